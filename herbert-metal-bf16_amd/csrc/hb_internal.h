@@ -1,0 +1,80 @@
+// hb_internal.h -- the host library's internal types: the context (the
+// reference's Gpu, src/metal/gpu.rs:22-124), the kernel descriptor's emitted
+// form (Emitted, src/msl/mod.rs:1461-1475) and the error channel.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include "herbert_hip.h"
+
+namespace hb {
+
+// Sets the thread's last error and returns `code`.
+int fail(int code, const std::string& msg);
+int hip_fail(hipError_t e, const char* what);
+
+#define HB_HIP(call)                                     \
+    do {                                                 \
+        hipError_t e_ = (call);                          \
+        if (e_ != hipSuccess) return hb::hip_fail(e_, #call); \
+    } while (0)
+
+// What a descriptor emits: the kernel's name (its cache key, as the
+// reference's Emitted::name), the source file and the -D constants hiprtc
+// compiles it with, its workgroup size and its bindings.
+struct Emitted {
+    std::string name;
+    std::string source;               // file name among the embedded sources
+    std::vector<std::string> defines; // "-DHB_K=2560", ...
+    uint32_t threads = 256;
+    uint32_t nbind = 0;
+};
+
+// Fills `e` for `d`, or returns an error (descriptor not implemented).
+int emit(const hb_desc& d, Emitted* e);
+// Workgroups of a launch of `d` over m rows (the reference's xxx_groups).
+uint32_t groups_of(const hb_desc& d, uint32_t m);
+// Checks the bindings' byte sizes against what `d` reads and writes over m
+// rows; returns HB_OK or an error naming the binding.
+int check_bindings(const hb_desc& d, const uint64_t* sizes, uint32_t nbind, uint32_t m);
+// Fills defaults of the descriptor's zero fields (tile sizes, ...).
+hb_desc with_defaults(const hb_desc& d);
+
+struct Buffer {
+    void* ptr = nullptr;
+    uint64_t size = 0;
+    bool live = false;
+};
+
+struct Kernel {
+    hb_desc desc;
+    Emitted em;
+    hipModule_t module = nullptr;
+    hipFunction_t fn = nullptr;
+};
+
+}  // namespace hb
+
+struct hb_gpu {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    hipEvent_t ev0 = nullptr, ev1 = nullptr;
+    std::vector<hb::Buffer> bufs;
+    std::vector<hb::Kernel> kernels;
+    std::unordered_map<std::string, int32_t> by_name;
+    std::string summary;
+    std::string arch;
+    double compile_seconds = 0.0;
+    hb::Kernel zero_kernel;  // the fill kernel of hb_zero
+    bool zero_built = false;
+};
+
+namespace hb {
+// Resolves a range to a device pointer and byte size (size 0 = to the end).
+int resolve(hb_gpu* g, const hb_range& r, char** ptr, uint64_t* size);
+}  // namespace hb

@@ -1,0 +1,444 @@
+// hb_runtime.cpp -- the HIP runtime under the C ABI: device context, buffer
+// arena, hiprtc kernel builds with an in-memory cache keyed by kernel name
+// and an on-disk code-object cache keyed by source hash, launches on the
+// context's stream and event timing.
+//
+// Reference: src/metal/gpu.rs (Gpu::open :70, alloc :150-157, pipeline
+// :127-148, dispatch :166-201, submit_wait :209-221) and the pipeline cache
+// QwenEngine::get (src/metal/qwen.rs:1156-1166).
+#include <hip/hiprtc.h>
+
+#include <chrono>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
+#include <sstream>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include "hb_internal.h"
+
+// The kernel sources, embedded by the build (name, text) pairs.
+#include "hb_sources.inc"
+
+namespace hb {
+
+static thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(HB_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+int resolve(hb_gpu* g, const hb_range& r, char** ptr, uint64_t* size) {
+    if (r.buf >= g->bufs.size() || !g->bufs[r.buf].live)
+        return fail(HB_ERR_INVALID, "range on buffer " + std::to_string(r.buf) + ": no such buffer");
+    const Buffer& b = g->bufs[r.buf];
+    if (r.offset > b.size || (r.size && r.offset + r.size > b.size))
+        return fail(HB_ERR_INVALID, "range [" + std::to_string(r.offset) + ", +" +
+                                        std::to_string(r.size) + ") outside buffer " +
+                                        std::to_string(r.buf) + " of " + std::to_string(b.size) +
+                                        " bytes");
+    *ptr = (char*)b.ptr + r.offset;
+    *size = r.size ? r.size : b.size - r.offset;
+    return HB_OK;
+}
+
+static const char* source_text(const std::string& name) {
+    for (const auto& s : kSources)
+        if (name == s.name) return s.text;
+    return nullptr;
+}
+
+static uint64_t fnv1a(const std::string& s, uint64_t h = 1469598103934665603ull) {
+    for (unsigned char c : s) {
+        h ^= c;
+        h *= 1099511628211ull;
+    }
+    return h;
+}
+
+static std::string cache_dir() {
+    const char* d = getenv("HB_CACHE_DIR");
+    if (d) return d;  // "" disables the disk cache
+    const char* home = getenv("HOME");
+    if (!home || !*home) return "";
+    return std::string(home) + "/.cache/herbert_hip";
+}
+
+static void mkdirs(const std::string& p) {
+    std::string cur;
+    std::stringstream ss(p);
+    std::string part;
+    if (!p.empty() && p[0] == '/') cur = "/";
+    while (std::getline(ss, part, '/')) {
+        if (part.empty()) continue;
+        cur += part + "/";
+        mkdir(cur.c_str(), 0755);
+    }
+}
+
+// Compiles `em` for `arch` with hiprtc; the code object into *code.
+static int compile(const Emitted& em, const std::string& arch, std::string* code) {
+    const char* text = source_text(em.source);
+    if (!text) return fail(HB_ERR_COMPILE, "no embedded source " + em.source);
+    std::vector<std::string> opts = {"--offload-arch=" + arch, "-O3", "-ffp-contract=off",
+                                     "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
+                                     "-packed-fp32-ops"};
+    for (const auto& d : em.defines) opts.push_back(d);
+    // The disk cache: the source, its headers and the options hashed.
+    std::string key = text;
+    for (const auto& s : kSources) key += s.text;
+    for (const auto& o : opts) key += "\n" + o;
+    int ver = 0;
+    hiprtcVersion(&ver, &ver);
+    key += "\nhiprtc" + std::to_string(HIP_VERSION);
+    char hex[32];
+    snprintf(hex, sizeof hex, "%016llx", (unsigned long long)fnv1a(key));
+    std::string dir = cache_dir();
+    std::string path = dir.empty() ? "" : dir + "/" + em.name + "-" + hex + ".co";
+    if (!path.empty()) {
+        std::ifstream f(path, std::ios::binary);
+        if (f) {
+            std::stringstream b;
+            b << f.rdbuf();
+            *code = b.str();
+            if (!code->empty()) return HB_OK;
+        }
+    }
+    std::vector<const char*> hnames, htexts;
+    for (const auto& s : kSources) {
+        if (em.source == s.name) continue;
+        hnames.push_back(s.name);
+        htexts.push_back(s.text);
+    }
+    hiprtcProgram prog;
+    hiprtcResult r = hiprtcCreateProgram(&prog, text, em.source.c_str(), (int)hnames.size(),
+                                         htexts.data(), hnames.data());
+    if (r != HIPRTC_SUCCESS)
+        return fail(HB_ERR_COMPILE, std::string("hiprtcCreateProgram: ") + hiprtcGetErrorString(r));
+    std::vector<const char*> copts;
+    for (const auto& o : opts) copts.push_back(o.c_str());
+    r = hiprtcCompileProgram(prog, (int)copts.size(), copts.data());
+    if (r != HIPRTC_SUCCESS) {
+        size_t n = 0;
+        hiprtcGetProgramLogSize(prog, &n);
+        std::string log(n, '\0');
+        if (n) hiprtcGetProgramLog(prog, &log[0]);
+        hiprtcDestroyProgram(&prog);
+        // Keep the first error lines: the reason a candidate is "not built".
+        std::string first;
+        std::stringstream ls(log);
+        std::string line;
+        int kept = 0;
+        while (std::getline(ls, line) && kept < 6) {
+            if (line.find("error") != std::string::npos || kept) {
+                first += line + "\n";
+                kept++;
+            }
+        }
+        return fail(HB_ERR_COMPILE, em.name + ": " + (first.empty() ? log : first));
+    }
+    size_t n = 0;
+    hiprtcGetCodeSize(prog, &n);
+    code->assign(n, '\0');
+    hiprtcGetCode(prog, &(*code)[0]);
+    hiprtcDestroyProgram(&prog);
+    if (!path.empty()) {
+        mkdirs(dir);
+        std::string tmp = path + ".tmp" + std::to_string(getpid());
+        {
+            std::ofstream f(tmp, std::ios::binary);
+            f.write(code->data(), (std::streamsize)code->size());
+        }
+        rename(tmp.c_str(), path.c_str());
+    }
+    return HB_OK;
+}
+
+static int load_kernel(hb_gpu* g, const hb_desc& d, Kernel* k) {
+    k->desc = d;
+    int rc = emit(d, &k->em);
+    if (rc) return rc;
+    auto t0 = std::chrono::steady_clock::now();
+    std::string code;
+    rc = compile(k->em, g->arch, &code);
+    if (rc) return rc;
+    HB_HIP(hipSetDevice(g->device));
+    HB_HIP(hipModuleLoadData(&k->module, code.data()));
+    HB_HIP(hipModuleGetFunction(&k->fn, k->module, "hb_kernel"));
+    g->compile_seconds +=
+        std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    return HB_OK;
+}
+
+static int launch_raw(hb_gpu* g, const Kernel& k, void** ptrs, uint32_t nptr, uint32_t m,
+                      uint32_t groups) {
+    if (groups == 0) return HB_OK;
+    // Kernel arguments: the binding pointers, then the launch's row count.
+    void* args[12];
+    for (uint32_t i = 0; i < nptr; i++) args[i] = &ptrs[i];
+    args[nptr] = &m;
+    HB_HIP(hipModuleLaunchKernel(k.fn, groups, 1, 1, k.em.threads, 1, 1, 0, g->stream, args,
+                                 nullptr));
+    return HB_OK;
+}
+
+static int launch(hb_gpu* g, int32_t kernel, const hb_range* b, uint32_t nbind, uint32_t m) {
+    if (kernel < 0 || (size_t)kernel >= g->kernels.size())
+        return fail(HB_ERR_INVALID, "no kernel " + std::to_string(kernel));
+    const Kernel& k = g->kernels[kernel];
+    if (nbind != k.em.nbind)
+        return fail(HB_ERR_INVALID, k.em.name + ": " + std::to_string(nbind) +
+                                        " bindings given, it takes " + std::to_string(k.em.nbind));
+    void* ptrs[10];
+    uint64_t sizes[10];
+    for (uint32_t i = 0; i < nbind; i++) {
+        char* p;
+        int rc = resolve(g, b[i], &p, &sizes[i]);
+        if (rc) return rc;
+        ptrs[i] = p;
+    }
+    int rc = check_bindings(k.desc, sizes, nbind, m);
+    if (rc) return fail(rc, k.em.name + ": " + hb_last_error());
+    return launch_raw(g, k, ptrs, nbind, m, groups_of(k.desc, m));
+}
+
+}  // namespace hb
+
+using namespace hb;
+
+extern "C" {
+
+const char* hb_last_error(void) { return g_last_error.c_str(); }
+
+int hb_open(int device, hb_gpu** out) {
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0) return fail(HB_ERR_NO_DEVICE, "no HIP device");
+    if (device < 0 || device >= n)
+        return fail(HB_ERR_INVALID, "device " + std::to_string(device) + " of " + std::to_string(n));
+    hb_gpu* g = new hb_gpu();
+    g->device = device;
+    hipDeviceProp_t p;
+    if ((e = hipSetDevice(device)) != hipSuccess || (e = hipGetDeviceProperties(&p, device)) != hipSuccess) {
+        delete g;
+        return hip_fail(e, "hipGetDeviceProperties");
+    }
+    std::string arch = p.gcnArchName;
+    g->arch = arch.substr(0, arch.find(':'));
+    if (g->arch != "gfx950") {
+        delete g;
+        return fail(HB_ERR_UNSUPPORTED, "device " + std::to_string(device) + " is " + arch +
+                                            ": the kernels are written for gfx950");
+    }
+    char buf[512];
+    snprintf(buf, sizeof buf, "%s, %d CUs, %.1f GiB, %s, LDS %zu KiB/workgroup", p.name,
+             p.multiProcessorCount, p.totalGlobalMem / 1073741824.0, p.gcnArchName,
+             (size_t)p.sharedMemPerBlock / 1024);
+    g->summary = buf;
+    if ((e = hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking)) != hipSuccess ||
+        (e = hipEventCreate(&g->ev0)) != hipSuccess || (e = hipEventCreate(&g->ev1)) != hipSuccess) {
+        delete g;
+        return hip_fail(e, "stream/event");
+    }
+    *out = g;
+    return HB_OK;
+}
+
+void hb_close(hb_gpu* g) {
+    if (!g) return;
+    hipSetDevice(g->device);
+    hipStreamSynchronize(g->stream);
+    for (auto& k : g->kernels)
+        if (k.module) hipModuleUnload(k.module);
+    if (g->zero_kernel.module) hipModuleUnload(g->zero_kernel.module);
+    for (auto& b : g->bufs)
+        if (b.live) hipFree(b.ptr);
+    hipEventDestroy(g->ev0);
+    hipEventDestroy(g->ev1);
+    hipStreamDestroy(g->stream);
+    delete g;
+}
+
+const char* hb_device_summary(hb_gpu* g) { return g ? g->summary.c_str() : ""; }
+
+int hb_alloc(hb_gpu* g, uint64_t bytes, hb_buf* out) {
+    if (!bytes) return fail(HB_ERR_INVALID, "hb_alloc of 0 bytes");
+    HB_HIP(hipSetDevice(g->device));
+    Buffer b;
+    // 256-byte aligned by hipMalloc; sizes rounded up to 256 so 128-bit
+    // loads of a last partial chunk stay inside the allocation.
+    HB_HIP(hipMalloc(&b.ptr, (bytes + 255) & ~255ull));
+    b.size = bytes;
+    b.live = true;
+    g->bufs.push_back(b);
+    *out = (hb_buf)(g->bufs.size() - 1);
+    return HB_OK;
+}
+
+int hb_free(hb_gpu* g, hb_buf buf) {
+    if (buf >= g->bufs.size() || !g->bufs[buf].live)
+        return fail(HB_ERR_INVALID, "hb_free: no buffer " + std::to_string(buf));
+    HB_HIP(hipStreamSynchronize(g->stream));
+    HB_HIP(hipFree(g->bufs[buf].ptr));
+    g->bufs[buf].live = false;
+    g->bufs[buf].ptr = nullptr;
+    return HB_OK;
+}
+
+int hb_buffer_ptr(hb_gpu* g, hb_buf buf, void** ptr) {
+    if (buf >= g->bufs.size() || !g->bufs[buf].live)
+        return fail(HB_ERR_INVALID, "no buffer " + std::to_string(buf));
+    *ptr = g->bufs[buf].ptr;
+    return HB_OK;
+}
+
+int hb_upload(hb_gpu* g, hb_buf buf, uint64_t offset, const void* src, uint64_t bytes) {
+    hb_range r{buf, 0, offset, bytes};
+    char* p;
+    uint64_t n;
+    int rc = resolve(g, r, &p, &n);
+    if (rc) return rc;
+    HB_HIP(hipMemcpyAsync(p, src, bytes, hipMemcpyHostToDevice, g->stream));
+    HB_HIP(hipStreamSynchronize(g->stream));
+    return HB_OK;
+}
+
+int hb_download(hb_gpu* g, hb_buf buf, uint64_t offset, void* dst, uint64_t bytes) {
+    hb_range r{buf, 0, offset, bytes};
+    char* p;
+    uint64_t n;
+    int rc = resolve(g, r, &p, &n);
+    if (rc) return rc;
+    HB_HIP(hipMemcpyAsync(dst, p, bytes, hipMemcpyDeviceToHost, g->stream));
+    HB_HIP(hipStreamSynchronize(g->stream));
+    return HB_OK;
+}
+
+int hb_zero(hb_gpu* g, hb_buf buf, uint64_t offset, uint64_t bytes) {
+    hb_range r{buf, 0, offset, bytes};
+    char* p;
+    uint64_t n;
+    int rc = resolve(g, r, &p, &n);
+    if (rc) return rc;
+    if (!g->zero_built) {
+        hb_desc d{};
+        d.kind = 0xffff;  // the fill kernel (emit's internal kind)
+        rc = load_kernel(g, d, &g->zero_kernel);
+        if (rc) return rc;
+        g->zero_built = true;
+    }
+    // Whole 16-byte words by the kernel, a ragged head or tail by copies.
+    uint64_t words = n / 16;
+    if (words) {
+        void* ptrs[2] = {p, nullptr};
+        uint32_t groups = (uint32_t)((words + 255) / 256);
+        if (words > 0xffffffffull || groups > 0x7fffffffu)
+            return fail(HB_ERR_INVALID, "hb_zero: too large");
+        void* args[3] = {&ptrs[0], &words, nullptr};
+        HB_HIP(hipModuleLaunchKernel(g->zero_kernel.fn, groups, 1, 1, 256, 1, 1, 0, g->stream,
+                                     args, nullptr));
+    }
+    if (n % 16) {
+        static const char zeros[16] = {0};
+        HB_HIP(hipMemcpyAsync(p + words * 16, zeros, n % 16, hipMemcpyHostToDevice, g->stream));
+    }
+    return HB_OK;
+}
+
+int hb_kernel_build(hb_gpu* g, const hb_desc* desc, int32_t* kernel) {
+    hb_desc d = with_defaults(*desc);
+    Emitted em;
+    int rc = emit(d, &em);
+    if (rc) return rc;
+    auto it = g->by_name.find(em.name);
+    if (it != g->by_name.end()) {
+        *kernel = it->second;
+        return HB_OK;
+    }
+    Kernel k;
+    rc = load_kernel(g, d, &k);
+    if (rc) return rc;
+    g->kernels.push_back(k);
+    *kernel = (int32_t)(g->kernels.size() - 1);
+    g->by_name[em.name] = *kernel;
+    return HB_OK;
+}
+
+const char* hb_kernel_name(hb_gpu* g, int32_t kernel) {
+    if (kernel < 0 || (size_t)kernel >= g->kernels.size()) return "";
+    return g->kernels[kernel].em.name.c_str();
+}
+
+uint32_t hb_kernel_groups(hb_gpu* g, int32_t kernel, uint32_t m) {
+    if (kernel < 0 || (size_t)kernel >= g->kernels.size()) return 0;
+    return groups_of(g->kernels[kernel].desc, m);
+}
+
+uint32_t hb_kernel_bindings(hb_gpu* g, int32_t kernel) {
+    if (kernel < 0 || (size_t)kernel >= g->kernels.size()) return 0;
+    return g->kernels[kernel].em.nbind;
+}
+
+double hb_compile_seconds(hb_gpu* g) { return g->compile_seconds; }
+
+int hb_launch(hb_gpu* g, int32_t kernel, const hb_range* b, uint32_t nbind, uint32_t m) {
+    return launch(g, kernel, b, nbind, m);
+}
+
+int hb_time(hb_gpu* g, const hb_op* ops, uint32_t nops, uint32_t reps, double* seconds) {
+    // Check every op once, then launch without re-checking.
+    struct Ready {
+        const Kernel* k;
+        void* ptrs[10];
+        uint32_t n, m, groups;
+    };
+    std::vector<Ready> ready(nops);
+    for (uint32_t i = 0; i < nops; i++) {
+        const hb_op& op = ops[i];
+        if (op.kernel < 0 || (size_t)op.kernel >= g->kernels.size())
+            return fail(HB_ERR_INVALID, "no kernel " + std::to_string(op.kernel));
+        const Kernel& k = g->kernels[op.kernel];
+        if (op.nbind != k.em.nbind || op.nbind > 8)
+            return fail(HB_ERR_INVALID, k.em.name + ": wrong number of bindings");
+        uint64_t sizes[10];
+        for (uint32_t j = 0; j < op.nbind; j++) {
+            char* p;
+            int rc = resolve(g, op.bind[j], &p, &sizes[j]);
+            if (rc) return rc;
+            ready[i].ptrs[j] = p;
+        }
+        int rc = check_bindings(k.desc, sizes, op.nbind, op.m);
+        if (rc) return fail(rc, k.em.name + ": " + hb_last_error());
+        ready[i].k = &k;
+        ready[i].n = op.nbind;
+        ready[i].m = op.m;
+        ready[i].groups = groups_of(k.desc, op.m);
+    }
+    HB_HIP(hipEventRecord(g->ev0, g->stream));
+    for (uint32_t r = 0; r < reps; r++)
+        for (auto& x : ready) {
+            int rc = launch_raw(g, *x.k, x.ptrs, x.n, x.m, x.groups);
+            if (rc) return rc;
+        }
+    HB_HIP(hipEventRecord(g->ev1, g->stream));
+    HB_HIP(hipEventSynchronize(g->ev1));
+    float ms = 0;
+    HB_HIP(hipEventElapsedTime(&ms, g->ev0, g->ev1));
+    *seconds = ms * 1e-3;
+    return HB_OK;
+}
+
+int hb_sync(hb_gpu* g) {
+    HB_HIP(hipStreamSynchronize(g->stream));
+    return HB_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,327 @@
+"""herbert_hip -- the Python host side of the MI355X bf16 matrix-multiplication
+path of herbert-metal-bf16, over the C ABI of libherbert_hip.so
+(include/herbert_hip.h) through ctypes.
+
+It mirrors the reference's Rust interface for this path, same names and
+argument meaning:
+  - Gpu            src/metal/gpu.rs:22-277 (open, alloc, alloc_with, pipeline,
+                   dispatch, submit_wait -> here launch / time_ops / sync)
+  - Range          src/metal/gpu.rs:40-57
+  - Out, MmaRows   src/metal/kernels.rs:30-43, src/metal/prefill.rs:317-338
+  - the emitters   gemm_mma_rows / gemm_mma_form (prefill.rs:418-431),
+                   gemm_simt (:133), gemm_mm2d (:442), gemm_nax_swiglu (:755),
+                   matvec / matvec_split (kernels.rs:146, 502), route_qwen,
+                   swiglu_slots, moe_combine (qwen_kernels.rs:1802, 2087,
+                   2119), moe_sort / moe_sort_atomic / moe_gather
+                   (prefill.rs:1315, 1450, 579): here they return a Desc,
+                   which Gpu.pipeline compiles (hiprtc, gfx950).
+  - Engine         the kernel-selection part of QwenEngine (qwen.rs): gemm,
+                   mv_full, expert_pipes, Tune.
+
+Errors raise HerbertError with the library's message (the reference's
+HerbertError::Backend(String), src/core/error.rs:9-27).  Nothing here falls
+back to the CPU: without libherbert_hip.so, importing the package raises.
+"""
+import ctypes
+import enum
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(os.path.dirname(_HERE), "libherbert_hip.so")
+
+
+class HerbertError(RuntimeError):
+    """A failing library call: the status code and the library's message."""
+
+    def __init__(self, code, msg):
+        super().__init__("herbert_hip error %d: %s" % (code, msg))
+        self.code = code
+        self.msg = msg
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            "libherbert_hip.so is not built (%s): run `python herbert-metal-bf16_amd/build.py` "
+            "or __graft_entry__.build()" % LIB_PATH)
+    return ctypes.CDLL(LIB_PATH)
+
+
+lib = _load()
+
+OK, ERR_INVALID, ERR_HIP, ERR_COMPILE, ERR_UNSUPPORTED, ERR_NO_DEVICE = 0, -1, -2, -3, -4, -5
+
+
+class Out(enum.IntEnum):
+    """Out (src/metal/kernels.rs:30-43)."""
+    Bf16 = 0
+    F32 = 1
+    Residual = 2
+
+
+class Kind(enum.IntEnum):
+    GEMM = 0
+    GEMM_SIMT = 1
+    GEMM_DIRECT = 2
+    GEMM_SWIGLU = 3
+    MATVEC = 4
+    ROUTE = 5
+    SORT = 6
+    SORT_ATOMIC = 7
+    GATHER = 8
+    SWIGLU = 9
+    COMBINE = 10
+
+
+class Rows(enum.IntEnum):
+    """MmaRows (src/metal/prefill.rs:317-338)."""
+    Dense = 0
+    Gather = 1
+    Scatter = 2
+
+
+class Range(ctypes.Structure):
+    """Range {buf, offset, size} (src/metal/gpu.rs:40-57); size 0 = to the end."""
+    _fields_ = [("buf", ctypes.c_uint32), ("reserved", ctypes.c_uint32),
+                ("offset", ctypes.c_uint64), ("size", ctypes.c_uint64)]
+
+    def __repr__(self):
+        return "Range(buf=%d, offset=%d, size=%d)" % (self.buf, self.offset, self.size)
+
+
+_DESC_FIELDS = ["kind", "k", "n", "out", "rows_of", "m_first", "bm", "bn", "bk", "wm", "wn",
+                "mfma", "dbuf", "swz", "order", "mv_m", "split", "persist", "rows", "form",
+                "top_k", "experts", "tiles", "rows_max"]
+
+
+class Desc(ctypes.Structure):
+    """hb_desc: a kernel's shape-keyed descriptor (what an emitter fixes)."""
+    _fields_ = [(f, ctypes.c_uint32) for f in _DESC_FIELDS] + [("reserved", ctypes.c_uint32 * 8)]
+
+    def __init__(self, **kw):
+        super().__init__()
+        for k, v in kw.items():
+            setattr(self, k, int(v))
+
+    def replace(self, **kw):
+        d = Desc(**{f: getattr(self, f) for f in _DESC_FIELDS})
+        for k, v in kw.items():
+            setattr(d, k, int(v))
+        return d
+
+    def __repr__(self):
+        return "Desc(%s)" % ", ".join("%s=%d" % (f, getattr(self, f)) for f in _DESC_FIELDS
+                                      if getattr(self, f))
+
+
+class Op(ctypes.Structure):
+    """Op {pipe, ranges, groups} (qwen.rs:650-655); the groups follow from m."""
+    _fields_ = [("kernel", ctypes.c_int32), ("m", ctypes.c_uint32), ("nbind", ctypes.c_uint32),
+                ("reserved", ctypes.c_uint32), ("bind", Range * 8)]
+
+    def __init__(self, kernel, ranges, m):
+        super().__init__()
+        self.kernel = int(kernel)
+        self.m = int(m)
+        self.nbind = len(ranges)
+        for i, r in enumerate(ranges):
+            self.bind[i] = r
+
+
+class MoeIo(ctypes.Structure):
+    _fields_ = [(f, Range) for f in ("state", "route", "list", "tiles", "x", "w_gate_up", "egu",
+                                     "ehb", "w_down", "ey", "xs")]
+
+
+_P = ctypes.c_void_p
+_u32, _u64, _i32 = ctypes.c_uint32, ctypes.c_uint64, ctypes.c_int32
+lib.hb_last_error.restype = ctypes.c_char_p
+lib.hb_open.argtypes = [ctypes.c_int, ctypes.POINTER(_P)]
+lib.hb_close.argtypes = [_P]
+lib.hb_close.restype = None
+lib.hb_device_summary.argtypes = [_P]
+lib.hb_device_summary.restype = ctypes.c_char_p
+lib.hb_alloc.argtypes = [_P, _u64, ctypes.POINTER(_u32)]
+lib.hb_free.argtypes = [_P, _u32]
+lib.hb_upload.argtypes = [_P, _u32, _u64, _P, _u64]
+lib.hb_download.argtypes = [_P, _u32, _u64, _P, _u64]
+lib.hb_zero.argtypes = [_P, _u32, _u64, _u64]
+lib.hb_buffer_ptr.argtypes = [_P, _u32, ctypes.POINTER(_P)]
+lib.hb_kernel_build.argtypes = [_P, ctypes.POINTER(Desc), ctypes.POINTER(_i32)]
+lib.hb_kernel_name.argtypes = [_P, _i32]
+lib.hb_kernel_name.restype = ctypes.c_char_p
+lib.hb_kernel_groups.argtypes = [_P, _i32, _u32]
+lib.hb_kernel_groups.restype = _u32
+lib.hb_kernel_bindings.argtypes = [_P, _i32]
+lib.hb_kernel_bindings.restype = _u32
+lib.hb_compile_seconds.argtypes = [_P]
+lib.hb_compile_seconds.restype = ctypes.c_double
+lib.hb_launch.argtypes = [_P, _i32, ctypes.POINTER(Range), _u32, _u32]
+lib.hb_time.argtypes = [_P, ctypes.POINTER(Op), _u32, _u32, ctypes.POINTER(ctypes.c_double)]
+lib.hb_sync.argtypes = [_P]
+lib.hb_fill_normal_bf16.argtypes = [_u64, ctypes.c_float, _P, _u64, ctypes.c_int]
+lib.hb_fill_normal_bf16.restype = None
+lib.hb_engine_open.argtypes = [_P, ctypes.c_char_p, ctypes.POINTER(_P)]
+lib.hb_engine_close.argtypes = [_P]
+lib.hb_engine_close.restype = None
+lib.hb_engine_tune_summary.argtypes = [_P]
+lib.hb_engine_tune_summary.restype = ctypes.c_char_p
+lib.hb_engine_buckets.argtypes = [_P, ctypes.POINTER(_u32), _u32, ctypes.POINTER(_u32)]
+lib.hb_engine_gemm.argtypes = [_P, _u32, _u32, _u32, Range, Range, Range, Range, _u32,
+                               ctypes.POINTER(_i32)]
+lib.hb_engine_matvec.argtypes = [_P, _u32, _u32, _u32, _u32, ctypes.POINTER(Range), _u32, Range,
+                                 Range, ctypes.POINTER(_i32)]
+lib.hb_engine_experts.argtypes = [_P, _u32, _u32, _u32, _u32, _u32, ctypes.POINTER(MoeIo),
+                                  ctypes.POINTER(_i32), ctypes.POINTER(_u32)]
+lib.hb_engine_autotune_seconds.argtypes = [_P]
+lib.hb_engine_autotune_seconds.restype = ctypes.c_double
+
+
+def last_error():
+    return lib.hb_last_error().decode(errors="replace")
+
+
+def check(rc):
+    if rc != OK:
+        raise HerbertError(rc, last_error())
+    return rc
+
+
+# ---- bf16 helpers (src/core/bf16.rs:7-23), vectorised ----
+
+def f32_to_bf16(a):
+    """Round to nearest even in integers: (bits + 0x7fff + lsb) >> 16."""
+    b = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+    return ((b + np.uint32(0x7FFF) + ((b >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)).astype(np.uint16)
+
+
+def bf16_to_f32(h):
+    return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+def normal_bf16(seed, std, shape, threads=None):
+    """bf16 bits ~ N(0, std^2) from the library's seeded generator."""
+    n = int(np.prod(shape))
+    out = np.empty(n, dtype=np.uint16)
+    lib.hb_fill_normal_bf16(int(seed), float(std), out.ctypes.data_as(_P), n,
+                            int(threads or min(16, os.cpu_count() or 1)))
+    return out.reshape(shape)
+
+
+# ---- the emitters: descriptors named after the reference's functions ----
+
+def moe_tiles(rows, top_k, experts, bm):
+    """moe_tiles (prefill.rs:832-835): the most expert tiles a block can need."""
+    return -(-rows * top_k // bm) + experts
+
+
+def gemm_mma_rows(kdim, n, out, m_first=True, rows_of=Rows.Dense, top_k=0, tiles=0, bm=0,
+                  experts=0, rows_max=0, **tile):
+    """gemm_mma_rows (prefill.rs:418-431): the MFMA GEMM over `rows_of`."""
+    return Desc(kind=Kind.GEMM, k=kdim, n=n, out=out, m_first=m_first, rows_of=rows_of,
+                top_k=top_k, tiles=tiles, bm=bm, experts=experts, rows_max=rows_max, **tile)
+
+
+def gemm_mma(kdim, n, out, m_first=True, **tile):
+    """gemm_mma (prefill.rs:418): the dense MFMA GEMM."""
+    return gemm_mma_rows(kdim, n, out, m_first, Rows.Dense, **tile)
+
+
+class Gpu:
+    """Gpu (src/metal/gpu.rs): one HIP device, its stream, buffers and kernels."""
+
+    def __init__(self, device=0):
+        h = _P()
+        check(lib.hb_open(int(device), ctypes.byref(h)))
+        self.h = h
+        self._sizes = {}
+
+    @classmethod
+    def open(cls, device=0):
+        return cls(device)
+
+    def close(self):
+        if self.h:
+            lib.hb_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def summary(self):
+        return lib.hb_device_summary(self.h).decode()
+
+    # memory
+    def alloc(self, nbytes):
+        b = _u32()
+        check(lib.hb_alloc(self.h, int(nbytes), ctypes.byref(b)))
+        self._sizes[b.value] = int(nbytes)
+        return b.value
+
+    def alloc_with(self, array):
+        a = np.ascontiguousarray(array)
+        b = self.alloc(max(a.nbytes, 1))
+        if a.nbytes:
+            self.upload(b, a)
+        return b
+
+    def free(self, buf):
+        check(lib.hb_free(self.h, int(buf)))
+        self._sizes.pop(int(buf), None)
+
+    def upload(self, buf, array, offset=0):
+        a = np.ascontiguousarray(array)
+        check(lib.hb_upload(self.h, int(buf), int(offset), a.ctypes.data_as(_P), a.nbytes))
+
+    def download(self, buf, dtype, count, offset=0):
+        out = np.empty(int(count), dtype=dtype)
+        check(lib.hb_download(self.h, int(buf), int(offset), out.ctypes.data_as(_P), out.nbytes))
+        return out
+
+    def zero(self, buf, offset=0, nbytes=None):
+        n = self._sizes[int(buf)] - offset if nbytes is None else nbytes
+        check(lib.hb_zero(self.h, int(buf), int(offset), int(n)))
+
+    def size(self, buf):
+        return self._sizes[int(buf)]
+
+    # kernels
+    def pipeline(self, desc):
+        """Gpu::pipeline: compile (hiprtc) or find the kernel `desc` names."""
+        k = _i32()
+        check(lib.hb_kernel_build(self.h, ctypes.byref(desc), ctypes.byref(k)))
+        return k.value
+
+    def kernel_name(self, k):
+        return lib.hb_kernel_name(self.h, int(k)).decode()
+
+    def groups(self, k, m):
+        return lib.hb_kernel_groups(self.h, int(k), int(m))
+
+    def compile_seconds(self):
+        return lib.hb_compile_seconds(self.h)
+
+    def launch(self, k, ranges, m):
+        """Gpu::dispatch over m rows (sizes checked by the library first)."""
+        arr = (Range * len(ranges))(*ranges)
+        check(lib.hb_launch(self.h, int(k), arr, len(ranges), int(m)))
+
+    def time_ops(self, ops, reps=1):
+        """time_ops (qwen.rs:2593): GPU seconds of `reps` runs of `ops`."""
+        arr = (Op * len(ops))(*ops)
+        s = ctypes.c_double()
+        check(lib.hb_time(self.h, arr, len(ops), int(reps), ctypes.byref(s)))
+        return s.value
+
+    def sync(self):
+        check(lib.hb_sync(self.h))
+
+
+def r(buf, offset=0, size=0):
+    """Range over a buffer (`Range::whole` when offset and size are 0)."""
+    return Range(int(buf), 0, int(offset), int(size))

@@ -1,0 +1,216 @@
+/*
+ * herbert_hip.h -- C ABI of the MI355X (gfx950) bf16 matrix-multiplication
+ * path of herbert-metal-bf16: the prefill block GEMM, the decode matvec and
+ * the MoE expert grouped GEMM with its route, sort, gather, SwiGLU and
+ * combine.  Plain pointers, sizes and integer status codes; no C++ or torch
+ * types cross it.  One context per device; a context is used by one host
+ * thread at a time (the reference's `Gpu` is not Send either), and work is
+ * ordered on the context's one HIP stream.
+ *
+ * Every entry point cites the reference interface it replaces, as
+ * path:line under src/ of xigh/herbert-metal-bf16.
+ */
+#ifndef HERBERT_HIP_H
+#define HERBERT_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes (the reference's HerbertError, core/error.rs:9-27) ---- */
+#define HB_OK 0
+#define HB_ERR_INVALID (-1)     /* bad argument: HerbertError::Config-like     */
+#define HB_ERR_HIP (-2)         /* HIP runtime failure: HerbertError::Backend  */
+#define HB_ERR_COMPILE (-3)     /* hiprtc failure: pipeline "not built"        */
+#define HB_ERR_UNSUPPORTED (-4) /* descriptor the kernels do not implement     */
+#define HB_ERR_NO_DEVICE (-5)   /* no HIP device                               */
+
+/* The message of the last failing call on this thread
+ * (HerbertError::Backend(String), core/error.rs:9-27). */
+const char *hb_last_error(void);
+
+/* ---- context: Gpu::open / summary / drop (metal/gpu.rs:22-124) ---- */
+typedef struct hb_gpu hb_gpu;
+
+/* Gpu::open (metal/gpu.rs:70): the HIP device `device`, its stream, its
+ * kernel cache. */
+int hb_open(int device, hb_gpu **gpu);
+/* Drop of Gpu: every buffer and module of the context freed. */
+void hb_close(hb_gpu *gpu);
+/* Gpu::summary (metal/gpu.rs:108): "name, CUs, memory, arch". */
+const char *hb_device_summary(hb_gpu *gpu);
+
+/* ---- memory: Gpu::alloc / alloc_with, Buffer, Range (metal/gpu.rs:59-67,
+ * 150-157).  The context owns every buffer until hb_free or hb_close. ---- */
+typedef uint32_t hb_buf;
+
+typedef struct hb_range { /* Range {buf, offset, size} (metal/gpu.rs:40-57) */
+    hb_buf buf;
+    uint32_t reserved;
+    uint64_t offset; /* bytes */
+    uint64_t size;   /* bytes; 0 = to the end of the buffer */
+} hb_range;
+
+int hb_alloc(hb_gpu *gpu, uint64_t bytes, hb_buf *out);
+int hb_free(hb_gpu *gpu, hb_buf buf);
+int hb_upload(hb_gpu *gpu, hb_buf buf, uint64_t offset, const void *src, uint64_t bytes);
+int hb_download(hb_gpu *gpu, hb_buf buf, uint64_t offset, void *dst, uint64_t bytes);
+/* Zero `bytes` at `offset` with a fill kernel on the context's stream. */
+int hb_zero(hb_gpu *gpu, hb_buf buf, uint64_t offset, uint64_t bytes);
+/* Device address of a buffer (for callers that bring their own kernels). */
+int hb_buffer_ptr(hb_gpu *gpu, hb_buf buf, void **ptr);
+
+/* ---- kernel descriptors: the emitter functions of the reference
+ * (prefill.rs, kernels.rs, qwen_kernels.rs) as one shape-keyed struct ---- */
+enum hb_kind {
+    HB_KIND_GEMM = 0,        /* gemm_mma_rows / gemm_mma_form (prefill.rs:418-431, 838-1307) */
+    HB_KIND_GEMM_SIMT = 1,   /* gemm_simt (prefill.rs:121-307) */
+    HB_KIND_GEMM_DIRECT = 2, /* gemm_mm2d / gemm_mm2d_rows (prefill.rs:442-569) */
+    HB_KIND_GEMM_SWIGLU = 3, /* gemm_nax_swiglu (prefill.rs:755-824) */
+    HB_KIND_MATVEC = 4,      /* matvec / matvec_split (kernels.rs:146-220, 502-519, 640-975) */
+    HB_KIND_ROUTE = 5,       /* route_qwen (qwen_kernels.rs:1802-1884) */
+    HB_KIND_SORT = 6,        /* moe_sort (prefill.rs:1315-1448) */
+    HB_KIND_SORT_ATOMIC = 7, /* moe_sort_atomic (prefill.rs:1450-1531) */
+    HB_KIND_GATHER = 8,      /* moe_gather (prefill.rs:579-610) */
+    HB_KIND_SWIGLU = 9,      /* swiglu_slots / swiglu_rows (qwen_kernels.rs:2087-2117) */
+    HB_KIND_COMBINE = 10     /* moe_combine (qwen_kernels.rs:2119-2165) */
+};
+
+enum hb_out { /* Out (kernels.rs:30-43) */
+    HB_OUT_BF16 = 0,
+    HB_OUT_F32 = 1,
+    HB_OUT_RESIDUAL = 2
+};
+
+enum hb_rows { /* MmaRows (prefill.rs:317-338) */
+    HB_ROWS_DENSE = 0,
+    HB_ROWS_GATHER = 1,
+    HB_ROWS_SCATTER = 2
+};
+
+typedef struct hb_desc {
+    uint32_t kind;    /* enum hb_kind */
+    uint32_t k, n;    /* K and N (per expert for the grouped GEMM); route: experts in n */
+    uint32_t out;     /* enum hb_out */
+    uint32_t rows_of; /* enum hb_rows (GEMM kinds) */
+    uint32_t m_first; /* tile_of (prefill.rs:31-43): walk row tiles first */
+    /* GEMM tile: bm rows of X x bn rows of W per workgroup, K by bk,
+     * wm x wn wavefronts, MFMA block 16 or 32, two LDS stages, LDS swizzle
+     * shift, tile order (0 plain, 1 XCD-contiguous). 0 = the kind's default. */
+    uint32_t bm, bn, bk, wm, wn, mfma, dbuf, swz, order;
+    /* matvec: rows of x (1..16), waves sharing a row block's K (split),
+     * persistent workgroups (0 = one per row block), W rows per wave
+     * (VALU form), form (0 VALU lanes-stride-K, 1 MFMA). */
+    uint32_t mv_m, split, persist, rows, form;
+    /* MoE: slots per row (top_k), experts, the tile table's capacity
+     * (moe_tiles, prefill.rs:832-835), rows of the largest block. */
+    uint32_t top_k, experts, tiles, rows_max;
+    uint32_t reserved[8];
+} hb_desc;
+
+/* Gpu::pipeline(&Emitted) (metal/gpu.rs:127-148) for the kernel the
+ * descriptor names: HIP C++ compiled by hiprtc for gfx950 with the shape as
+ * constants, cached by name in the context (QwenEngine::get, qwen.rs:1156-1166)
+ * and on disk by source hash.  *kernel is the pipeline's index. */
+int hb_kernel_build(hb_gpu *gpu, const hb_desc *desc, int32_t *kernel);
+/* Emitted::name: the descriptor in the reference's naming
+ * (gemm_mma_{K}x{N}_{bf16|f32|res}..., prefill.rs:1295-1300). */
+const char *hb_kernel_name(hb_gpu *gpu, int32_t kernel);
+/* The xxx_groups grid functions (gemm_mma_groups prefill.rs:406,
+ * gemm_mma_expert_groups :826, matvec_groups kernels.rs:1456, ...): the
+ * workgroups of a launch over `m` rows. */
+uint32_t hb_kernel_groups(hb_gpu *gpu, int32_t kernel, uint32_t m);
+/* Bindings the kernel takes, in order (Emitted::bindings). */
+uint32_t hb_kernel_bindings(hb_gpu *gpu, int32_t kernel);
+/* Seconds spent compiling so far ([metal] line, qwen.rs:1069). */
+double hb_compile_seconds(hb_gpu *gpu);
+
+/* Gpu::dispatch (metal/gpu.rs:166-201) of one kernel over `m` rows on the
+ * context's stream: the bindings' sizes are checked against the descriptor
+ * and m before anything runs.  Bindings per kind:
+ *   GEMM, GEMM_DIRECT, GEMM_SIMT, GEMM_SWIGLU: state, W, X, Y[, list, tiles]
+ *   MATVEC: W, x, y          ROUTE: scores, route
+ *   SORT, SORT_ATOMIC: state, route, list, tiles
+ *   GATHER: state, list, X, XS        SWIGLU: gate_up, h
+ *   COMBINE: y, route, out
+ * `m` is the rows of the block (the kernels read state[3], never beyond m). */
+int hb_launch(hb_gpu *gpu, int32_t kernel, const hb_range *bindings, uint32_t nbind, uint32_t m);
+
+typedef struct hb_op { /* Op {pipe, ranges, groups} (qwen.rs:650-655) */
+    int32_t kernel;
+    uint32_t m;
+    uint32_t nbind;
+    uint32_t reserved;
+    hb_range bind[8];
+} hb_op;
+
+/* time_ops (qwen.rs:2593): `reps` runs of `ops` in order on the stream,
+ * timed by two HIP events on that stream; *seconds = the GPU time of all. */
+int hb_time(hb_gpu *gpu, const hb_op *ops, uint32_t nops, uint32_t reps, double *seconds);
+/* submit_wait (metal/gpu.rs:209-221): wait for the stream. */
+int hb_sync(hb_gpu *gpu);
+
+/* ---- synthetic inputs (host side, no GPU) ---- */
+/* n bf16 values ~ N(0, std^2): splitmix64(seed) -> two uniforms -> Box-Muller
+ * in double -> f32 -> round to nearest even; element i is a function of
+ * (seed, i) only, so any thread count gives the same bits. */
+void hb_fill_normal_bf16(uint64_t seed, float std, uint16_t *out, uint64_t n, int threads);
+
+/* ---- the selection layer: QwenEngine's kernel choice (qwen.rs) ---- */
+typedef struct hb_engine hb_engine;
+
+/* Tune::default + Tune::apply (qwen.rs:62-389) on `tune` ("key=value,..."),
+ * over the context `gpu`.  HB_ERR_INVALID with the reference's message on a
+ * bad key or value. */
+int hb_engine_open(hb_gpu *gpu, const char *tune, hb_engine **engine);
+void hb_engine_close(hb_engine *engine);
+/* Tune::summary (qwen.rs:391-398) of the settings this path reads. */
+const char *hb_engine_tune_summary(hb_engine *engine);
+/* The prefill buckets (qwen.rs:1051-1063): 64*2^i below prefill.block, then
+ * prefill.block; *count of them written to out (capacity cap). */
+int hb_engine_buckets(hb_engine *engine, uint32_t *out, uint32_t cap, uint32_t *count);
+
+/* QwenEngine::gemm (qwen.rs:2200-2325): the kernel of Y[m][n] = X[m][k].W^T
+ * written as `out`: the one gemm.mma/gemm.tn/gemm.mform name, or with
+ * gemm.auto every candidate checked against the first (check_candidates,
+ * qwen.rs:2497-2545: max|err| <= max|ref|/64 at m and m - m/3 - 3 rows) and
+ * the fastest eligible kept (pick_flagged, qwen.rs:2547-2575), cached under
+ * "{k}x{n} {Out}, {m} rows".  W, X, Y and the 16-byte state are the buffers
+ * timed on (state[3] and Y restored afterwards).  Logs [autotune] lines. */
+int hb_engine_gemm(hb_engine *engine, uint32_t k, uint32_t n, uint32_t out, hb_range state,
+                   hb_range w, hb_range x, hb_range y, uint32_t m, int32_t *kernel);
+
+/* QwenEngine::mv_full (qwen.rs:1311-1511) for M rows of x: with mv.auto the
+ * forms timed over every matrix of the shape (`ws`, mv.cold) and the fastest
+ * kept under "{k}x{n} {Out}"; else the form mv.split/mv.persist name. */
+int hb_engine_matvec(hb_engine *engine, uint32_t k, uint32_t n, uint32_t out, uint32_t mv_m,
+                     const hb_range *ws, uint32_t nws, hb_range x, hb_range y, int32_t *kernel);
+
+/* QwenEngine::expert_pipes (qwen.rs:2326-2391): the sort, the grouped
+ * gate_up GEMM (Gather) and down GEMM (Scatter) of an MoE layer of `experts`
+ * experts, top_k slots, hidden `hidden`, expert intermediate `inter`, for
+ * blocks of m rows: with gemm.auto, tiles of 16, 32 and 64 rows (moe.tile
+ * only, if given) each timed, the tile whose kernels sum the least kept.
+ * Buffers: state, route [m][2*top_k], list, tiles, X [m][hidden], the
+ * experts' gate_up W [experts*2*inter][hidden], EGU [m*top_k][2*inter],
+ * EHB [m*top_k][inter], down W [experts*hidden][inter], EY
+ * [m*top_k][hidden], XS [m*top_k][hidden] (the gather's output).
+ * kernels[0..3] = sort, gate_up GEMM, down GEMM, gather (-1: gate_up reads
+ * X through the list itself); *bm = rows per tile. */
+typedef struct hb_moe_io {
+    hb_range state, route, list, tiles, x, w_gate_up, egu, ehb, w_down, ey, xs;
+} hb_moe_io;
+int hb_engine_experts(hb_engine *engine, uint32_t experts, uint32_t top_k, uint32_t hidden,
+                      uint32_t inter, uint32_t m, const hb_moe_io *io, int32_t kernels[4],
+                      uint32_t *bm);
+
+/* Seconds the engine spent timing candidates (autotune_seconds). */
+double hb_engine_autotune_seconds(hb_engine *engine);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HERBERT_HIP_H */

@@ -1,0 +1,63 @@
+"""Tolerance checks of the numerical contract, shared by the parity tests.
+
+The contract: each output within 2 bf16 ulp of
+the CPU oracle's (scalar f32 accumulation in increasing k, one RNE), and
+within the reference's own gate max|err| <= max|ref|/64
+(src/metal/qwen.rs:2497-2545).  Near zero, where cancellation makes 2 ulp of
+a tiny result meaningless, the per-element bound also admits the f32
+rounding bound of two summation orders, 2*gamma_K*sum|x_k w_k| with
+gamma_K = K*u/(1-K*u), u = 2^-24 (Higham, Accuracy and Stability of
+Numerical Algorithms, 2nd ed., eq. 3.5).
+"""
+import numpy as np
+
+
+def bf16_to_f32(h):
+    return (np.asarray(h, dtype=np.uint16).astype(np.uint32) << np.uint32(16)).view(np.float32)
+
+
+def bf16_ulp(v):
+    """The spacing of bf16 numbers at |v| (8 significant bits)."""
+    a = np.abs(np.asarray(v, dtype=np.float64))
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -126)))
+    return 2.0 ** (e - 7)
+
+
+def gamma(k):
+    u = 2.0 ** -24
+    return k * u / (1 - k * u)
+
+
+def abs_products(x, w, rows=None):
+    """sum_k |x_k w_k| per output, in float64 (rows: the X rows to use)."""
+    xf = np.abs(bf16_to_f32(x).astype(np.float64))
+    wf = np.abs(bf16_to_f32(w).astype(np.float64))
+    if rows is not None:
+        xf = xf[rows]
+    return xf @ wf.T
+
+
+def check_close(got, want, k, absprod, what="", ulps=2.0):
+    """Asserts the contract; returns a dict of statistics for the report."""
+    g = bf16_to_f32(got).astype(np.float64) if got.dtype == np.uint16 else got.astype(np.float64)
+    t = bf16_to_f32(want).astype(np.float64) if want.dtype == np.uint16 else want.astype(np.float64)
+    assert g.shape == t.shape, (g.shape, t.shape)
+    assert np.all(np.isfinite(g)), what + ": non-finite outputs"
+    err = np.abs(g - t)
+    bound = ulps * bf16_ulp(np.maximum(np.abs(g), np.abs(t))) + 2 * gamma(k) * absprod
+    bad = err > bound
+    scale = max(np.abs(t).max(), 1e-6)
+    stats = {
+        "n": int(err.size),
+        "exact": float(np.mean(err == 0)),
+        "max_err": float(err.max()),
+        "max_ulp": float((err / bf16_ulp(np.maximum(np.abs(t), 2.0 ** -126))).max()),
+        "gate": float(err.max() / scale),
+    }
+    if bad.any():
+        i = np.argwhere(bad)[0]
+        raise AssertionError("%s: %d of %d outputs beyond 2 ulp + f32 bound, first at %s: got %r "
+                             "want %r bound %r" % (what, int(bad.sum()), bad.size, tuple(i),
+                                                   g[tuple(i)], t[tuple(i)], bound[tuple(i)]))
+    assert err.max() <= scale / 64, what + ": beyond the 1/64-of-max gate"
+    return stats
