@@ -54,6 +54,8 @@ hb_desc with_defaults(const hb_desc& in) {
         if (!d.mv_m) d.mv_m = 1;
         if (!d.split) d.split = 1;
         if (!d.rows) d.rows = 4;
+        if (!d.unroll) d.unroll = 4;
+        if (d.form == 1) d.rows = 16;
     }
     return d;
 }
@@ -82,6 +84,14 @@ int emit(const hb_desc& d, Emitted* e) {
             bool experts = d.rows_of != HB_ROWS_DENSE;
             if (experts && (!d.top_k || !d.experts || !d.tiles))
                 return fail(HB_ERR_INVALID, "gemm over experts: top_k, experts and tiles");
+            e->threads = 64 * d.wm * d.wn;
+            // LDS swizzle shift: 0 = the conflict-free one for gfx950's 64
+            // banks (256-byte lines hold 16/CH rows of CH chunks: rows
+            // r >> log2(16/CH) apart get distinct chunk slots); s+1 = s.
+            uint32_t ch = d.bk / 8, shift = 0;
+            if (d.swz) shift = d.swz - 1;
+            else
+                for (uint32_t v = 16 / (ch < 16 ? ch : 16); v > 1; v >>= 1) shift++;
             std::string rows;
             if (d.rows_of == HB_ROWS_GATHER) {
                 snprintf(name, sizeof name, "_gather_k%u_t%u_m%u", d.top_k, d.tiles, d.bm);
@@ -90,9 +100,13 @@ int emit(const hb_desc& d, Emitted* e) {
                 snprintf(name, sizeof name, "_scatter_t%u_m%u", d.tiles, d.bm);
                 rows = name;
             }
-            snprintf(name, sizeof name, "gemm_mma_%ux%u_%s%s_t%ux%u_k%u_w%ux%u_x%u%s_s%u_o%u%s", d.k,
-                     d.n, out_tag(d.out), d.m_first ? "_mf" : "", d.bn, d.bm, d.bk, d.wn, d.wm,
-                     d.mfma, d.dbuf ? "_d" : "", d.swz, d.order, rows.c_str());
+            if (d.dbuf > 3 || (!d.lds_dma && d.dbuf > 1))
+                return fail(HB_ERR_UNSUPPORTED, "gemm: stages 1..4 (1..2 through registers)");
+            if (d.lds_dma && ((d.bm * d.bk / 8) % e->threads || (d.bn * d.bk / 8) % e->threads))
+                return fail(HB_ERR_UNSUPPORTED, "gemm: direct-to-LDS staging needs whole chunks per lane");
+            snprintf(name, sizeof name, "gemm_mma_%ux%u_%s%s_t%ux%u_k%u_w%ux%u_x%u_d%u%s_s%u_o%u%s",
+                     d.k, d.n, out_tag(d.out), d.m_first ? "_mf" : "", d.bn, d.bm, d.bk, d.wn, d.wm,
+                     d.mfma, d.dbuf, d.lds_dma ? "_dma" : "", shift, d.order, rows.c_str());
             e->name = name;
             e->source = "gemm_mfma.hip";
             e->threads = 64 * d.wm * d.wn;
@@ -101,10 +115,91 @@ int emit(const hb_desc& d, Emitted* e) {
                           D("HB_ROWS", d.rows_of), D("HB_TOPK", experts ? d.top_k : 1),
                           D("HB_BM", d.bm),      D("HB_BN", d.bn),     D("HB_BK", d.bk),
                           D("HB_WM", d.wm),      D("HB_WN", d.wn),     D("HB_MFMA", d.mfma),
-                          D("HB_DBUF", d.dbuf ? 1 : 0), D("HB_SWZ", d.swz),
-                          D("HB_ORDER", d.order), D("HB_MFIRST", d.m_first ? 1 : 0)};
+                          D("HB_STAGES", d.dbuf + 1), D("HB_SWZ", shift),
+                          D("HB_ORDER", d.order), D("HB_MFIRST", d.m_first ? 1 : 0),
+                          D("HB_DMA", d.lds_dma ? 1 : 0)};
             return HB_OK;
         }
+        case HB_KIND_MATVEC: {
+            if (d.out > HB_OUT_RESIDUAL || d.form > 1)
+                return fail(HB_ERR_INVALID, "matvec: out / form out of range");
+            if (!d.k || !d.n || d.k % (8 * d.split) || (d.split != 1 && d.split != 2 && d.split != 4))
+                return fail(HB_ERR_UNSUPPORTED, "matvec: K a multiple of 8*split, split 1, 2 or 4");
+            if (d.form == 0 && (d.rows > 8 || !d.rows || d.rows * d.mv_m > 64 || d.mv_m > 16))
+                return fail(HB_ERR_UNSUPPORTED, "matvec: rows 1..8, rows*m <= 64");
+            if (d.form == 1 && (d.mv_m > 16 || (d.k / d.split) % 32))
+                return fail(HB_ERR_UNSUPPORTED, "matvec (MFMA): m <= 16, K/split a multiple of 32");
+            if (!d.unroll || d.unroll > 8)
+                return fail(HB_ERR_UNSUPPORTED, "matvec: unroll 1..8");
+            snprintf(name, sizeof name, "matvec_%ux%u%s_r%u_k%u%s_m%u_%s_u%u", d.k, d.n,
+                     d.out == HB_OUT_F32 ? "_f32" : d.out == HB_OUT_RESIDUAL ? "_res" : "", d.rows,
+                     d.split, d.persist ? ("_p" + std::to_string(d.persist)).c_str() : "", d.mv_m,
+                     d.form ? "mfma" : "valu", d.unroll);
+            e->name = name;
+            e->source = "matvec.hip";
+            e->threads = 256;
+            e->nbind = 3;
+            e->defines = {D("HB_K", d.k),         D("HB_N", d.n),          D("HB_OUT", d.out),
+                          D("HB_MV_M", d.mv_m),   D("HB_FORM", d.form),    D("HB_ROWS", d.rows),
+                          D("HB_SPLIT", d.split), D("HB_PERSIST", d.persist), D("HB_UNROLL", d.unroll)};
+            return HB_OK;
+        }
+        case HB_KIND_ROUTE:
+            if (!d.experts || d.experts % 64 || d.experts > 1024 || !d.top_k || d.top_k > 64 ||
+                d.top_k > d.experts)
+                return fail(HB_ERR_UNSUPPORTED, "route: experts a multiple of 64 up to 1024, top_k <= 64");
+            snprintf(name, sizeof name, "route_qwen_%u_k%u", d.experts, d.top_k);
+            e->name = name;
+            e->source = "moe.hip";
+            e->threads = 256;
+            e->nbind = 2;
+            e->defines = {D("HB_OP", 1), D("HB_E", d.experts), D("HB_TOPK", d.top_k), D("HB_D", 8)};
+            return HB_OK;
+        case HB_KIND_SORT:
+        case HB_KIND_SORT_ATOMIC: {
+            if (!d.experts || d.experts > 1024 || !d.top_k || !d.bm || !d.rows_max)
+                return fail(HB_ERR_UNSUPPORTED, "sort: experts <= 1024, top_k, bm, rows_max");
+            uint32_t tiles = cdiv(d.rows_max * d.top_k, d.bm) + d.experts;  // moe_tiles
+            if (d.tiles && d.tiles < tiles)
+                return fail(HB_ERR_INVALID, "sort: tile table smaller than moe_tiles");
+            bool atomic = d.kind == HB_KIND_SORT_ATOMIC;
+            snprintf(name, sizeof name, "moe_sort%s_%u_k%u_r%u_m%u", atomic ? "_atomic" : "",
+                     d.experts, d.top_k, d.rows_max, d.bm);
+            e->name = name;
+            e->source = "moe.hip";
+            e->threads = 1024;
+            e->nbind = 4;
+            e->defines = {D("HB_OP", atomic ? 3 : 2), D("HB_E", d.experts), D("HB_TOPK", d.top_k),
+                          D("HB_BM", d.bm), D("HB_D", 8)};
+            return HB_OK;
+        }
+        case HB_KIND_GATHER:
+            if (!d.n || d.n % 8 || !d.top_k) return fail(HB_ERR_UNSUPPORTED, "gather: hidden a multiple of 8");
+            snprintf(name, sizeof name, "moe_gather_%u_k%u", d.n, d.top_k);
+            e->name = name;
+            e->source = "moe.hip";
+            e->threads = 256;
+            e->nbind = 4;
+            e->defines = {D("HB_OP", 4), D("HB_E", 64), D("HB_TOPK", d.top_k), D("HB_D", d.n)};
+            return HB_OK;
+        case HB_KIND_SWIGLU:
+            if (!d.n || d.n % 8) return fail(HB_ERR_UNSUPPORTED, "swiglu: n a multiple of 8");
+            snprintf(name, sizeof name, "swiglu_%u", d.n);
+            e->name = name;
+            e->source = "moe.hip";
+            e->threads = 256;
+            e->nbind = 2;
+            e->defines = {D("HB_OP", 5), D("HB_E", 64), D("HB_TOPK", 1), D("HB_D", d.n)};
+            return HB_OK;
+        case HB_KIND_COMBINE:
+            if (!d.n || d.n % 8 || !d.top_k) return fail(HB_ERR_UNSUPPORTED, "combine: d a multiple of 8");
+            snprintf(name, sizeof name, "moe_combine_%u_k%u", d.n, d.top_k);
+            e->name = name;
+            e->source = "moe.hip";
+            e->threads = 256;
+            e->nbind = 3;
+            e->defines = {D("HB_OP", 6), D("HB_E", 64), D("HB_TOPK", d.top_k), D("HB_D", d.n)};
+            return HB_OK;
         default:
             return fail(HB_ERR_UNSUPPORTED, "kernel kind " + std::to_string(d.kind) + " not built");
     }
@@ -120,6 +215,21 @@ uint32_t groups_of(const hb_desc& d, uint32_t m) {
             if (d.rows_of != HB_ROWS_DENSE) return d.tiles * nt;  // gemm_mma_expert_groups
             return cdiv(m, d.bm) * nt;                               // gemm_mma_groups
         }
+        case HB_KIND_MATVEC: {  // matvec_groups / matvec_split_groups
+            uint32_t rb = d.form == 1 ? 16 : d.rows, per = 4 / d.split;
+            uint32_t wgs = cdiv(cdiv(d.n, rb), per);
+            return d.persist ? (d.persist < wgs ? d.persist : wgs) : wgs;
+        }
+        case HB_KIND_ROUTE:
+            return cdiv(m, 4);  // a wavefront per row
+        case HB_KIND_SORT:
+        case HB_KIND_SORT_ATOMIC:
+            return 1;
+        case HB_KIND_GATHER:
+            return (uint32_t)(((uint64_t)m * d.top_k * (d.n / 8) + 255) / 256);
+        case HB_KIND_SWIGLU:
+        case HB_KIND_COMBINE:
+            return (uint32_t)(((uint64_t)m * (d.n / 8) + 255) / 256);
         default:
             return 0;
     }
@@ -157,6 +267,46 @@ int check_bindings(const hb_desc& d, const uint64_t* s, uint32_t nbind, uint32_t
             if (d.rows_max && m > d.rows_max)
                 return fail(HB_ERR_INVALID, "m beyond the kernel's rows_max");
         }
+        return HB_OK;
+    }
+    if (m == 0) return fail(HB_ERR_INVALID, "0 rows");
+    uint64_t mm = m, k2 = 2ull * d.top_k;
+    switch (d.kind) {
+        case HB_KIND_ROUTE:
+            if ((rc = need(s, 0, mm * d.experts * 2, "scores"))) return rc;
+            return need(s, 1, mm * k2 * 4, "route");
+        case HB_KIND_SORT:
+        case HB_KIND_SORT_ATOMIC: {
+            if (m > d.rows_max) return fail(HB_ERR_INVALID, "sort: m beyond rows_max");
+            uint64_t tiles = cdiv(d.rows_max * d.top_k, d.bm) + d.experts;
+            if ((rc = need(s, 0, 16, "state"))) return rc;
+            if ((rc = need(s, 1, mm * k2 * 4, "route"))) return rc;
+            if ((rc = need(s, 2, mm * d.top_k * 4, "list"))) return rc;
+            return need(s, 3, (1 + 3 * tiles) * 4, "tiles");
+        }
+        case HB_KIND_GATHER:
+            if ((rc = need(s, 0, 16, "state"))) return rc;
+            if ((rc = need(s, 1, mm * d.top_k * 4, "list"))) return rc;
+            if ((rc = need(s, 2, mm * d.n * 2, "X"))) return rc;
+            return need(s, 3, mm * d.top_k * d.n * 2, "XS");
+        case HB_KIND_SWIGLU:
+            if ((rc = need(s, 0, mm * 2 * d.n * 2, "gate_up"))) return rc;
+            return need(s, 1, mm * d.n * 2, "h");
+        case HB_KIND_COMBINE:
+            if ((rc = need(s, 0, mm * d.top_k * d.n * 2, "y"))) return rc;
+            if ((rc = need(s, 1, mm * k2 * 4, "route"))) return rc;
+            return need(s, 2, mm * d.n * 2, "out");
+        default:
+            break;
+    }
+    if (d.kind == HB_KIND_MATVEC) {
+        uint64_t k = d.k, n = d.n;
+        if (m > d.mv_m)
+            return fail(HB_ERR_INVALID, "matvec of " + std::to_string(m) + " rows: 1.." +
+                                            std::to_string(d.mv_m));
+        if ((rc = need(s, 0, n * k * 2, "W"))) return rc;
+        if ((rc = need(s, 1, mm * k * 2, "x"))) return rc;
+        if ((rc = need(s, 2, mm * n * out_bytes(d.out), "y"))) return rc;
         return HB_OK;
     }
     return fail(HB_ERR_UNSUPPORTED, "kind " + std::to_string(d.kind));

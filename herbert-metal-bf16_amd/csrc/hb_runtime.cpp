@@ -95,8 +95,6 @@ static int compile(const Emitted& em, const std::string& arch, std::string* code
     std::string key = text;
     for (const auto& s : kSources) key += s.text;
     for (const auto& o : opts) key += "\n" + o;
-    int ver = 0;
-    hiprtcVersion(&ver, &ver);
     key += "\nhiprtc" + std::to_string(HIP_VERSION);
     char hex[32];
     snprintf(hex, sizeof hex, "%016llx", (unsigned long long)fnv1a(key));

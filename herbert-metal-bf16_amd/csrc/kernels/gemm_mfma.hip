@@ -17,14 +17,24 @@
 //    of a fragment (16 or 32 rows at one chunk) hits distinct banks; the
 //    global loads are 128-bit and coalesced (CH consecutive lanes read one
 //    row's BK elements).
-//  - HB_DBUF: two LDS stages, the next K tile's global loads in flight while
-//    the current one is multiplied, one barrier per K tile.
+//  - HB_DMA 1: the tiles go straight from global memory into LDS (gfx950's
+//    buffer_load_dwordx4 ... lds) through HB_STAGES stages: the loads of K tile
+//    kt + STAGES - 1 are issued while tile kt is multiplied, so the memory
+//    latency is covered by STAGES - 1 tiles of MFMA work; the barrier that
+//    publishes tile kt + 1 sits inside the last MFMA step of tile kt, so the
+//    first fragments of tile kt + 1 are read while those MFMAs run.
+//    HB_DMA 0: staging through registers (global_load, ds_write), one or two
+//    stages; the form for tiles whose chunk count is not a multiple of the
+//    workgroup's lanes.
+//  - Within a stage, the fragments of MFMA step s+1 are read while step s's
+//    MFMAs run, interleaved by scheduling groups.
 //  - HB_ORDER 1: the workgroup index remapped so each XCD works on a
 //    contiguous range of tiles (its own L2 keeps their panels).
 //
 // Compile-time constants (-D): HB_K, HB_N, HB_OUT (0 bf16, 1 f32, 2
 // residual), HB_ROWS (0 dense, 1 gather, 2 scatter), HB_TOPK, HB_BM, HB_BN,
-// HB_BK, HB_WM, HB_WN, HB_MFMA (16|32), HB_DBUF, HB_SWZ, HB_ORDER, HB_MFIRST.
+// HB_BK, HB_WM, HB_WN, HB_MFMA (16|32), HB_STAGES (1..4), HB_SWZ, HB_ORDER,
+// HB_MFIRST, HB_DMA.
 //
 // Bindings: state (u32[4], state[3] = rows), W, X, Y, list, tiles; then the
 // rows the launch was sized for (m_launch).  Dense: rows past m read the
@@ -40,19 +50,24 @@ constexpr u32 WM = HB_WM, WN = HB_WN, NT = 64 * WM * WN;
 constexpr u32 FM = HB_MFMA;
 constexpr u32 TM = BM / WM, TN = BN / WN;
 constexpr u32 IM = TM / FM, IN = TN / FM;
-constexpr u32 CH = BK / 8;                 // 16-byte chunks of a staged row
-constexpr u32 KS = FM == 16 ? 32 : 16;     // K of one MFMA
+constexpr u32 CH = BK / 8;                  // 16-byte chunks of a staged row
+constexpr u32 KS = FM == 16 ? 32 : 16;      // K of one MFMA
+constexpr u32 S = BK / KS;                  // MFMA steps per staged tile
 constexpr u32 KT = K / BK;
 constexpr u32 NTILES = (N + BN - 1) / BN;
-constexpr u32 XCH = BM * CH, WCH = BN * CH; // chunks per stage
+constexpr u32 XCH = BM * CH, WCH = BN * CH;  // chunks per stage
 constexpr u32 X_LD = (XCH + NT - 1) / NT, W_LD = (WCH + NT - 1) / NT;
-constexpr u32 NBUF = HB_DBUF ? 2 : 1;
+constexpr u32 NS = HB_STAGES;
 
 static_assert(K % BK == 0, "K a multiple of the K step");
 static_assert(N % 4 == 0, "N a multiple of 4");
 static_assert(TM % FM == 0 && TN % FM == 0, "wave tile a multiple of the MFMA block");
 static_assert(BK % KS == 0 && (CH & (CH - 1)) == 0, "K step");
 static_assert(NT % CH == 0, "threads a multiple of the chunks of a row");
+static_assert(NS >= 1 && NS <= 4, "1 to 4 stages");
+static_assert(!HB_DMA || (XCH % NT == 0 && WCH % NT == 0),
+              "direct-to-LDS staging: every lane loads the same number of chunks");
+static_assert(HB_DMA || NS <= 2, "register staging: 1 or 2 stages");
 
 typedef __attribute__((ext_vector_type(FM == 16 ? 4 : 16))) float acc_t;
 
@@ -65,6 +80,17 @@ HB_DEV acc_t mfma(bf16x8 a, bf16x8 b, acc_t c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 #endif
 }
+
+// s_waitcnt with vmcnt(n) and the other counters left alone (gfx9
+// encoding: vmcnt[3:0] bits 3:0, vmcnt[5:4] bits 15:14, expcnt 6:4,
+// lgkmcnt 11:8).
+#define WAIT_VM(n) __builtin_amdgcn_s_waitcnt((((n) & 15) | (((n) >> 4) << 14) | (7 << 4) | (15 << 8)))
+// The workgroup barrier of the staged pipeline: this wave's LDS reads done
+// and (by a WAIT_VM before it) its tile's direct-to-LDS loads landed, then
+// s_barrier.  Not __syncthreads(): its release fence would also wait for
+// the later stages' loads still in flight.  The "memory" clobber keeps the
+// compiler from moving LDS accesses across it.
+#define STAGE_BARRIER() asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory")
 
 // Four consecutive outputs (columns n..n+3 of row `yrow`), as Out says
 // (src/metal/kernels.rs:223-236).
@@ -87,14 +113,23 @@ HB_DEV void store4(void* Yv, u64 at, float v0, float v1, float v2, float v3) {
     }
 }
 
+#define HB_INLINE __attribute__((always_inline))
+
 extern "C" __global__ __launch_bounds__(NT) void hb_kernel(
     const u32* __restrict__ state, const u16* __restrict__ W, const u16* __restrict__ X,
     void* __restrict__ Yv, const u32* __restrict__ list, const u32* __restrict__ tiles,
     u32 m_launch) {
-    __shared__ u32x4 sX[NBUF][XCH];
-    __shared__ u32x4 sW[NBUF][WCH];
+    // The stages as distinct LDS objects, so that the compiler sees that one
+    // stage's direct-to-LDS loads never alias another stage's reads.
+    __shared__ u32x4 sX0[XCH], sW0[WCH];
+    __shared__ u32x4 sX1[NS > 1 ? XCH : 1], sW1[NS > 1 ? WCH : 1];
+    __shared__ u32x4 sX2[NS > 2 ? XCH : 1], sW2[NS > 2 ? WCH : 1];
+    __shared__ u32x4 sX3[NS > 3 ? XCH : 1], sW3[NS > 3 ? WCH : 1];
+#define STX(i) ((i) == 0 ? sX0 : (i) == 1 ? sX1 : (i) == 2 ? sX2 : sX3)
+#define STW(i) ((i) == 0 ? sW0 : (i) == 1 ? sW1 : (i) == 2 ? sW2 : sW3)
 
-    const u32 tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const u32 tid = threadIdx.x, lane = tid & 63u;
+    const u32 wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar
     const u32 wm = wave % WM, wn = wave / WM;
     u32 g = blockIdx.x;
     if (HB_ORDER == 1) g = xcd_remap(g, gridDim.x);
@@ -102,9 +137,8 @@ extern "C" __global__ __launch_bounds__(NT) void hb_kernel(
     // The tile: its first row (dense row or sorted pair), its rows, its
     // column tile and its expert.
     u32 row0, rows, gn, expert = 0;
-    u32 m = m_launch;
     if constexpr (ROWS == 0) {
-        m = rows_of_state(state, m_launch);
+        const u32 m = rows_of_state(state, m_launch);
         const u32 mb = (m + BM - 1) / BM;
         u32 gm;
         if (HB_MFIRST) { gm = g % mb; gn = g / mb; }
@@ -126,54 +160,42 @@ extern "C" __global__ __launch_bounds__(NT) void hb_kernel(
     const u32 n0 = gn * BN;
 
     // Global element offsets of this thread's chunks (row clamped to the
-    // last valid one), per K tile advanced by BK.
-    const u32 c = tid % CH;
+    // last valid one), advanced by BK per K tile.  Register staging: chunk
+    // id = tid + q*NT is (row id/CH, chunk id%CH), written to its swizzled
+    // place.  Direct-to-LDS staging: lane l of a wave writes LDS slot base +
+    // l, so slot p = tid + q*NT holds (row p/CH, chunk (p%CH) ^
+    // swizzle(row)) and the lane loads that chunk.
+    auto x_row = [&](u32 r) HB_INLINE -> u32 {
+        if (r >= BM) r = BM - 1;
+        u32 rr = r < rows ? r : rows - 1;
+        if constexpr (ROWS == 1) {
+            u32 pr = list[row0 + rr] / TOPK;
+            return pr < m_launch ? pr : m_launch - 1;
+        } else if constexpr (ROWS == 2) {
+            u32 p = row0 + rr;
+            return p < pairs ? p : pairs - 1;
+        } else {
+            return row0 + rr;
+        }
+    };
+    auto w_row = [&](u32 r) HB_INLINE -> u32 {
+        if (r >= BN) r = BN - 1;
+        u32 n = n0 + r;
+        return expert * N + (n < N ? n : N - 1);
+    };
     u32 xoff[X_LD], woff[W_LD];
 #pragma unroll
     for (u32 q = 0; q < X_LD; q++) {
-        u32 r = tid / CH + q * (NT / CH);
-        if (r >= BM) r = BM - 1;
-        u32 rr = r < rows ? r : rows - 1;
-        u32 xrow;
-        if constexpr (ROWS == 1) {
-            u32 pr = list[row0 + rr] / TOPK;
-            xrow = pr < m_launch ? pr : m_launch - 1;
-        } else if constexpr (ROWS == 2) {
-            u32 p = row0 + rr;
-            xrow = p < pairs ? p : pairs - 1;
-        } else {
-            xrow = row0 + rr;
-        }
-        xoff[q] = xrow * K + c * 8;
+        const u32 p = tid + q * NT, r = p / CH;
+        const u32 cc = HB_DMA ? ((p % CH) ^ ((r >> HB_SWZ) & (CH - 1))) : p % CH;
+        xoff[q] = x_row(r) * K + cc * 8;
     }
 #pragma unroll
     for (u32 q = 0; q < W_LD; q++) {
-        u32 r = tid / CH + q * (NT / CH);
-        if (r >= BN) r = BN - 1;
-        u32 n = n0 + r;
-        if (n >= N) n = N - 1;
-        woff[q] = (expert * N + n) * K + c * 8;
+        const u32 p = tid + q * NT, r = p / CH;
+        const u32 cc = HB_DMA ? ((p % CH) ^ ((r >> HB_SWZ) & (CH - 1))) : p % CH;
+        woff[q] = w_row(r) * K + cc * 8;
     }
-
-    u32x4 rx[X_LD], rw[W_LD];
-    auto load = [&](u32 kt) {
-#pragma unroll
-        for (u32 q = 0; q < X_LD; q++) rx[q] = *(const u32x4*)(X + xoff[q] + kt * BK);
-#pragma unroll
-        for (u32 q = 0; q < W_LD; q++) rw[q] = *(const u32x4*)(W + (u64)woff[q] + kt * BK);
-    };
-    auto stage = [&](u32 buf) {
-#pragma unroll
-        for (u32 q = 0; q < X_LD; q++) {
-            u32 id = tid + q * NT;
-            if (XCH % NT == 0 || id < XCH) sX[buf][lpos(id / CH, id % CH)] = rx[q];
-        }
-#pragma unroll
-        for (u32 q = 0; q < W_LD; q++) {
-            u32 id = tid + q * NT;
-            if (WCH % NT == 0 || id < WCH) sW[buf][lpos(id / CH, id % CH)] = rw[q];
-        }
-    };
 
     acc_t acc[IN][IM];
 #pragma unroll
@@ -182,42 +204,186 @@ extern "C" __global__ __launch_bounds__(NT) void hb_kernel(
         for (u32 j = 0; j < IM; j++) acc[i][j] = acc_t{};
 
     const u32 fr = lane % FM, fc = lane / FM;
-    auto multiply = [&](u32 buf) {
+    // Fragment addressing: lane (fr, fc) reads rows base + i*FM + fr at
+    // chunk s*(KS/8) + fc of every step s.  The swizzle term of those rows is
+    // the lane's own ((fr >> SWZ) & (CH-1)) whatever i and the wave (the row
+    // offsets are multiples of CH << SWZ), so each read is a per-lane base
+    // plus a per-step chunk plus a constant: few live address registers.
+    static_assert(((FM >> HB_SWZ) % CH) == 0 && ((TN >> HB_SWZ) % CH) == 0 &&
+                      ((TM >> HB_SWZ) % CH) == 0,
+                  "fragment rows keep the lane's swizzle");
+    const u32 fsw = (fr >> HB_SWZ) & (CH - 1);
+    const u32 wbase = (wn * TN + fr) * CH, xbase = (wm * TM + fr) * CH;
+    bf16x8 a[2][IN], b[2][IM];
+    // Step s's fragments of a stage into a[h], b[h]: IN of W (A operand), IM
+    // of X (B operand).
+    auto read_frags = [&](const u32x4* sX, const u32x4* sW, u32 s, u32 h) HB_INLINE {
+        const u32 ch = (s * (KS / 8) + fc) ^ fsw;
 #pragma unroll
-        for (u32 s = 0; s < BK / KS; s++) {
-            const u32 ch = s * (KS / 8) + fc;
-            bf16x8 a[IN], b[IM];
+        for (u32 i = 0; i < IN; i++)
+            a[h][i] = __builtin_bit_cast(bf16x8, sW[wbase + ch + i * FM * CH]);
 #pragma unroll
-            for (u32 i = 0; i < IN; i++)
-                a[i] = __builtin_bit_cast(bf16x8, sW[buf][lpos(wn * TN + i * FM + fr, ch)]);
+        for (u32 j = 0; j < IM; j++)
+            b[h][j] = __builtin_bit_cast(bf16x8, sX[xbase + ch + j * FM * CH]);
+    };
+    auto mfmas = [&](u32 h) HB_INLINE {
 #pragma unroll
-            for (u32 j = 0; j < IM; j++)
-                b[j] = __builtin_bit_cast(bf16x8, sX[buf][lpos(wm * TM + j * FM + fr, ch)]);
+        for (u32 i = 0; i < IN; i++)
 #pragma unroll
-            for (u32 i = 0; i < IN; i++)
+            for (u32 j = 0; j < IM; j++) acc[i][j] = mfma(a[h][i], b[h][j], acc[i][j]);
+    };
+    // One LDS read, then IN*IM/(IN+IM) MFMAs, in turn.
+    auto interleave = [&]() HB_INLINE {
+        constexpr u32 NR = IN + IM, NM = IN * IM, PER = NM / NR ? NM / NR : 1;
 #pragma unroll
-                for (u32 j = 0; j < IM; j++) acc[i][j] = mfma(a[i], b[j], acc[i][j]);
+        for (u32 q = 0; q < NR; q++) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+            __builtin_amdgcn_sched_group_barrier(0x008, PER, 0);  // MFMA
         }
     };
+    // Steps 0..S-2 of a stage whose step-0 fragments are in a[0], b[0].
+    auto steps = [&](const u32x4* sX, const u32x4* sW) HB_INLINE {
+#pragma unroll
+        for (u32 s = 0; s + 1 < S; s++) {
+            __builtin_amdgcn_sched_barrier(0);
+            read_frags(sX, sW, s + 1, (s + 1) & 1);
+            mfmas(s & 1);
+            interleave();
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
 
-    load(0);
-    stage(0);
-    __syncthreads();
-    for (u32 kt = 0; kt < KT; kt++) {
-        const u32 cur = NBUF == 2 ? (kt & 1u) : 0u;
-        if (kt + 1 < KT) load(kt + 1);
-        multiply(cur);
-        if constexpr (NBUF == 2) {
-            if (kt + 1 < KT) stage(cur ^ 1u);
-            __syncthreads();
-        } else {
-            __syncthreads();
-            if (kt + 1 < KT) {
-                stage(0);
-                __syncthreads();
+#if HB_DMA
+    // Buffer loads straight into LDS: the base in a scalar resource, one
+    // 32-bit byte offset per chunk, the K tile's advance as scalar offset,
+    // the wave's LDS slot in m0.  Issued as inline asm so that the compiler's
+    // wait-count pass, which cannot tell the stages apart, does not wait for
+    // every stage in flight before each LDS read; the waits are the
+    // pipeline's own (WAIT_VM / STAGE_BARRIER).
+    const __amdgpu_buffer_rsrc_t rX =
+        __builtin_amdgcn_make_buffer_rsrc((void*)X, (short)0, 0x7fffffff, 0x00020000);
+    const __amdgpu_buffer_rsrc_t rW =
+        __builtin_amdgcn_make_buffer_rsrc((void*)W, (short)0, 0x7fffffff, 0x00020000);
+    typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
+    auto lds_addr = [&](u32x4* p) HB_INLINE -> u32 {
+        return (u32)(u64)(lds_u32x4*)p;
+    };
+    auto load_stage = [&](u32 kt, u32x4* sX, u32x4* sW) HB_INLINE {
+        const u32 kb = kt * BK * 2;
+#pragma unroll
+        for (u32 q = 0; q < X_LD; q++)
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                         :: "s"(lds_addr(&sX[q * NT + wave * 64])), "v"(xoff[q] * 2), "s"(rX),
+                            "s"(kb) : "memory");
+#pragma unroll
+        for (u32 q = 0; q < W_LD; q++)
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+                         :: "s"(lds_addr(&sW[q * NT + wave * 64])), "v"(woff[q] * 2), "s"(rW),
+                            "s"(kb) : "memory");
+    };
+    constexpr u32 LDT = X_LD + W_LD;  // load instructions per tile per lane
+    // Prologue: tiles 0..NS-2 in flight, tile 0 landed and published.
+#pragma unroll
+    for (u32 t = 0; t + 1 < NS; t++)
+        if (t < KT) load_stage(t, STX(t), STW(t));
+    if (NS == 1) load_stage(0, sX0, sW0);
+    if (NS > 2 && KT > NS - 2) WAIT_VM((NS - 2) * LDT);
+    else WAIT_VM(0);
+    STAGE_BARRIER();
+    read_frags(sX0, sW0, 0, 0);
+
+    // KT is a multiple of NS (NS > 1), so every unrolled tile runs the same
+    // code: one MFMA site per step keeps the accumulators in AGPRs.  Past
+    // the last tile the "next" fragments are read from a stale stage and
+    // never used.
+    static_assert(NS == 1 || KT % NS == 0, "K tiles a multiple of the stages");
+    for (u32 kt0 = 0; kt0 < KT; kt0 += NS) {
+#pragma unroll
+        for (u32 bi = 0; bi < NS; bi++) {
+            const u32 kt = kt0 + bi;
+            u32x4* cx = STX(bi);
+            u32x4* cw = STW(bi);
+            if constexpr (NS > 1) {
+                // Tile kt + NS - 1 into the stage tile kt - 1 used; every wave
+                // passed the barrier after its last read of it.
+                if (kt + NS - 1 < KT)
+                    load_stage(kt + NS - 1, STX((bi + NS - 1) % NS), STW((bi + NS - 1) % NS));
+                steps(cx, cw);
+                // Tile kt + 1 landed (its loads are the oldest in flight),
+                // published, and its first fragments read under the last
+                // MFMAs of tile kt.
+                if (kt + NS - 1 < KT) WAIT_VM((NS - 2) * LDT);
+                else WAIT_VM(0);
+                STAGE_BARRIER();
+                read_frags(STX((bi + 1) % NS), STW((bi + 1) % NS), 0, S & 1);
+                mfmas((S - 1) & 1);
+                interleave();
+                __builtin_amdgcn_sched_barrier(0);
+            } else {
+                steps(cx, cw);
+                // One stage: every wave done with it, then the next tile.
+                STAGE_BARRIER();
+                if (kt + 1 < KT) load_stage(kt + 1, sX0, sW0);
+                WAIT_VM(0);
+                STAGE_BARRIER();
+                read_frags(sX0, sW0, 0, S & 1);
+                mfmas((S - 1) & 1);
+            }
+            // The next tile's step 0 is in a[S & 1]; steps() expects a[0].
+            if constexpr (S & 1) {
+#pragma unroll
+                for (u32 i = 0; i < IN; i++) a[0][i] = a[1][i];
+#pragma unroll
+                for (u32 j = 0; j < IM; j++) b[0][j] = b[1][j];
             }
         }
     }
+#else
+    u32x4 rx[X_LD], rw[W_LD];
+    auto load = [&](u32 kt) HB_INLINE {
+#pragma unroll
+        for (u32 q = 0; q < X_LD; q++)
+            if (XCH % NT == 0 || tid + q * NT < XCH) rx[q] = *(const u32x4*)(X + xoff[q] + kt * BK);
+#pragma unroll
+        for (u32 q = 0; q < W_LD; q++)
+            if (WCH % NT == 0 || tid + q * NT < WCH) rw[q] = *(const u32x4*)(W + (u64)woff[q] + kt * BK);
+    };
+    auto stage = [&](u32x4* sX, u32x4* sW) HB_INLINE {
+#pragma unroll
+        for (u32 q = 0; q < X_LD; q++) {
+            u32 id = tid + q * NT;
+            if (XCH % NT == 0 || id < XCH) sX[lpos(id / CH, id % CH)] = rx[q];
+        }
+#pragma unroll
+        for (u32 q = 0; q < W_LD; q++) {
+            u32 id = tid + q * NT;
+            if (WCH % NT == 0 || id < WCH) sW[lpos(id / CH, id % CH)] = rw[q];
+        }
+    };
+    auto tile = [&](u32 kt, u32x4* cx, u32x4* cw, u32x4* nx, u32x4* nw) HB_INLINE {
+        if (kt + 1 < KT) load(kt + 1);
+        // Keep the next tile's loads ahead of the multiplies (the scheduler
+        // would otherwise sink them next to their LDS stores).
+        __builtin_amdgcn_sched_barrier(0);
+        read_frags(cx, cw, 0, 0);
+        steps(cx, cw);
+        mfmas((S - 1) & 1);
+        if (NS == 1) __syncthreads();
+        if (kt + 1 < KT) stage(nx, nw);
+        __syncthreads();
+    };
+    load(0);
+    stage(sX0, sW0);
+    __syncthreads();
+    if constexpr (NS == 2) {
+        for (u32 kt = 0; kt < KT; kt += 2) {
+            tile(kt, sX0, sW0, sX1, sW1);
+            if (kt + 1 < KT) tile(kt + 1, sX1, sW1, sX0, sW0);
+        }
+    } else {
+        for (u32 kt = 0; kt < KT; kt++) tile(kt, sX0, sW0, sX0, sW0);
+    }
+#endif
 
     // Epilogue: lane holds, per MFMA block, runs of 4 columns of one row.
 #pragma unroll
@@ -237,8 +403,7 @@ extern "C" __global__ __launch_bounds__(NT) void hb_kernel(
             for (u32 q = 0; q < FM * FM / 256; q++) {
                 // FM 16: one run, columns 4*fc..+3 of the block; FM 32: four
                 // runs, columns q*8 + 4*fc..+3.
-                const u32 nl = wn * TN + i * FM + q * 8 + 4 * fc;
-                const u32 n = n0 + nl;
+                const u32 n = n0 + wn * TN + i * FM + q * 8 + 4 * fc;
                 if (n < N) {
                     const acc_t& v = acc[i][j];
                     store4(Yv, (u64)yrow * N + n, v[4 * q], v[4 * q + 1], v[4 * q + 2],

@@ -1,0 +1,232 @@
+// matvec.hip -- the decode projection y[m][N] = x[m][K] . W[N][K]^T for the
+// few rows m of a decode step (m <= MV_M), bf16 operands, f32 sums, Out's
+// epilogue.  HBM-bound: W is streamed once per launch.
+//
+// Reference: src/metal/kernels.rs:146-220 (matvec: a simdgroup per `rows`
+// rows, lanes striding K by 8 bf16, an fma chain per lane, the simdgroup
+// sum), :502-519 and :640-975 (matvec_split: `split` simdgroups sharing a
+// row's K, partials folded in simdgroup order, persistent groups), :223-236
+// (store).  The reference decodes one row; m up to MV_M is this build's
+// extension (one W read serves every row).
+//
+// Two forms (HB_FORM):
+//  0 (VALU, the reference's arithmetic layout): a wavefront computes ROWS
+//    consecutive rows of W over its K range; lane l takes the 16-byte
+//    chunks l, l+64, ... of it, UNROLL chunks per row in flight; then a
+//    butterfly sum over the 64 lanes.
+//  1 (MFMA): a wavefront computes 16 rows of W with
+//    v_mfma_f32_16x16x32_bf16, W the A operand (the lane's 16-byte chunks
+//    loaded straight from memory as the operand, no conversion), x the B
+//    operand (rows past m are zeros).  Lane (r, q) of a step of 32 K holds
+//    row r's elements q*8*UNROLL + u*8.. of a UNROLL-step block, so each
+//    lane reads 16*UNROLL contiguous bytes; x uses the same K mapping.
+//    UNROLL independent accumulators, summed at the end.
+// Both: SPLIT wavefronts of a workgroup share a row block's K (contiguous
+// ranges); their partials are added in wave order through LDS.  PERSIST
+// > 0: that many workgroups loop over the row blocks.
+//
+// Constants: HB_K, HB_N, HB_OUT, HB_MV_M, HB_FORM, HB_ROWS (form 0),
+// HB_SPLIT, HB_PERSIST, HB_UNROLL.  Bindings: W, x, y; then m (<= MV_M).
+#include "hb_common.h"
+
+constexpr u32 K = HB_K, N = HB_N, MV = HB_MV_M;
+constexpr int OUT = HB_OUT;
+constexpr u32 SPLIT = HB_SPLIT, U = HB_UNROLL;
+constexpr u32 WAVES = 4, NT = 256;
+constexpr u32 GROUPS_PER_WG = WAVES / SPLIT;  // row blocks per workgroup
+#if HB_FORM == 0
+constexpr u32 RB = HB_ROWS;                   // rows per row block
+#else
+constexpr u32 RB = 16;
+#endif
+constexpr u32 WG_ROWS = RB * GROUPS_PER_WG;
+constexpr u32 NBLK = (N + RB - 1) / RB;
+constexpr u32 KS = K / SPLIT;                 // K of one wave's range
+
+static_assert(WAVES % SPLIT == 0, "split divides the waves");
+static_assert(K % (8 * SPLIT) == 0 && KS % 8 == 0, "K split in whole chunks");
+static_assert(HB_FORM == 0 || (MV <= 16 && KS % 32 == 0), "MFMA form: m <= 16, K steps of 32");
+
+HB_DEV void store_out(void* y, u64 at, float v) {
+    if constexpr (OUT == 1) {
+        ((float*)y)[at] = v;
+    } else if constexpr (OUT == 2) {
+        u16* p = (u16*)y + at;
+        *p = (u16)f32_to_bf16(bf16_to_f32(*p) + round_bf16(v));
+    } else {
+        ((u16*)y)[at] = (u16)f32_to_bf16(v);
+    }
+}
+
+HB_DEV float wave_sum(float v) {
+    // Butterfly over the 64 lanes (xor 32, 16, ..., 1).
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) v += __shfl_xor(v, s, 64);
+    return v;
+}
+
+extern "C" __global__ __launch_bounds__(NT) void hb_kernel(const u16* __restrict__ W,
+                                                           const u16* __restrict__ x,
+                                                           void* __restrict__ y, u32 m_launch) {
+    __shared__ float part[SPLIT > 1 ? WAVES * RB * 16 : 1];
+    const u32 tid = threadIdx.x, lane = tid & 63u;
+    const u32 wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const u32 gi = wave / SPLIT, sp = wave % SPLIT;  // row block in the group, K part
+    const u32 m = m_launch < MV ? m_launch : MV;
+    const u32 k0 = sp * KS;
+    const u32 nwg = (NBLK + GROUPS_PER_WG - 1) / GROUPS_PER_WG;
+    const u32 step = HB_PERSIST ? gridDim.x : nwg;
+
+    for (u32 wg = blockIdx.x; wg < nwg; wg += step) {
+        const u32 blk = wg * GROUPS_PER_WG + gi;
+        const u32 n0 = blk * RB;
+#if HB_FORM == 0
+        // ---- VALU: ROWS rows, lanes over 16-byte chunks ----
+        float acc[RB][MV];
+#pragma unroll
+        for (u32 r = 0; r < RB; r++)
+#pragma unroll
+            for (u32 j = 0; j < MV; j++) acc[r][j] = 0.0f;
+        const u16* wr[RB];
+#pragma unroll
+        for (u32 r = 0; r < RB; r++) {
+            u32 n = n0 + r;
+            wr[r] = W + (u64)(n < N ? n : N - 1) * K;
+        }
+        constexpr u32 CHUNKS = KS / 8;
+        u32 c = lane;
+        for (; c + 64 * (U - 1) < CHUNKS; c += 64 * U) {
+            u32x4 wv[U][RB];
+#pragma unroll
+            for (u32 u = 0; u < U; u++)
+#pragma unroll
+                for (u32 r = 0; r < RB; r++)
+                    wv[u][r] = __builtin_nontemporal_load((const u32x4*)(wr[r] + k0 + (c + 64 * u) * 8));
+#pragma unroll
+            for (u32 u = 0; u < U; u++) {
+#pragma unroll
+                for (u32 j = 0; j < MV; j++) {
+                    if (j >= m) break;
+                    const u32x4 xv = *(const u32x4*)(x + (u64)j * K + k0 + (c + 64 * u) * 8);
+#pragma unroll
+                    for (u32 r = 0; r < RB; r++) {
+                        float a = acc[r][j];
+#pragma unroll
+                        for (u32 e = 0; e < 4; e++) {
+                            a = __builtin_fmaf(bf16_lo(wv[u][r][e]), bf16_lo(xv[e]), a);
+                            a = __builtin_fmaf(bf16_hi(wv[u][r][e]), bf16_hi(xv[e]), a);
+                        }
+                        acc[r][j] = a;
+                    }
+                }
+            }
+        }
+        for (; c < CHUNKS; c += 64) {
+#pragma unroll
+            for (u32 j = 0; j < MV; j++) {
+                if (j >= m) break;
+                const u32x4 xv = *(const u32x4*)(x + (u64)j * K + k0 + c * 8);
+#pragma unroll
+                for (u32 r = 0; r < RB; r++) {
+                    const u32x4 wv = *(const u32x4*)(wr[r] + k0 + c * 8);
+                    float a = acc[r][j];
+#pragma unroll
+                    for (u32 e = 0; e < 4; e++) {
+                        a = __builtin_fmaf(bf16_lo(wv[e]), bf16_lo(xv[e]), a);
+                        a = __builtin_fmaf(bf16_hi(wv[e]), bf16_hi(xv[e]), a);
+                    }
+                    acc[r][j] = a;
+                }
+            }
+        }
+#pragma unroll
+        for (u32 r = 0; r < RB; r++)
+#pragma unroll
+            for (u32 j = 0; j < MV; j++) acc[r][j] = wave_sum(acc[r][j]);
+        // Lane r*MV + j owns (row r, x row j).
+        float mine = 0.0f;
+#pragma unroll
+        for (u32 r = 0; r < RB; r++)
+#pragma unroll
+            for (u32 j = 0; j < MV; j++)
+                if (lane == r * MV + j) mine = acc[r][j];
+        const u32 own_r = lane / MV, own_j = lane % MV;
+        const bool owner = lane < RB * MV;
+#else
+        // ---- MFMA: 16 rows x (m <= 16) columns per wave ----
+        const u32 fr = lane & 15u, fq = lane >> 4;
+        u32 n = n0 + fr;
+        const u16* wrow = W + (u64)(n < N ? n : N - 1) * K + k0;
+        const bool xon = fr < m;
+        const u16* xrow = x + (u64)(xon ? fr : 0) * K + k0;
+        f32x4 acc[U];
+#pragma unroll
+        for (u32 u = 0; u < U; u++) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        constexpr u32 BLOCK = 32 * U;  // K per unrolled block
+        u32 kk = 0;
+        for (; kk + BLOCK <= KS; kk += BLOCK) {
+            u32x4 wv[U], xv[U];
+#pragma unroll
+            for (u32 u = 0; u < U; u++)
+                wv[u] = __builtin_nontemporal_load((const u32x4*)(wrow + kk + fq * 8 * U + u * 8));
+#pragma unroll
+            for (u32 u = 0; u < U; u++)
+                xv[u] = xon ? *(const u32x4*)(xrow + kk + fq * 8 * U + u * 8) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (u32 u = 0; u < U; u++)
+                acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wv[u]),
+                                                                 __builtin_bit_cast(bf16x8, xv[u]),
+                                                                 acc[u], 0, 0, 0);
+        }
+        for (; kk < KS; kk += 32) {
+            const u32x4 wv = *(const u32x4*)(wrow + kk + fq * 8);
+            const u32x4 xv = xon ? *(const u32x4*)(xrow + kk + fq * 8) : u32x4{0u, 0u, 0u, 0u};
+            acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wv),
+                                                             __builtin_bit_cast(bf16x8, xv), acc[0],
+                                                             0, 0, 0);
+        }
+#pragma unroll
+        for (u32 u = 1; u < U; u++) acc[0] += acc[u];
+        // Lane (fr, fq) holds rows 4*fq..+3 of the block for x row fr.
+#endif
+
+        // ---- fold the SPLIT partials in wave order, then Out ----
+#if HB_FORM == 0
+        if constexpr (SPLIT > 1) {
+            if (owner) part[(wave * RB + own_r) * 16 + own_j] = mine;
+            __syncthreads();
+            if (sp == 0 && owner) {
+                float s = 0.0f;
+#pragma unroll
+                for (u32 q = 0; q < SPLIT; q++) s += part[((gi * SPLIT + q) * RB + own_r) * 16 + own_j];
+                mine = s;
+            }
+        }
+        if (sp == 0 && owner && own_j < m && n0 + own_r < N)
+            store_out(y, (u64)own_j * N + n0 + own_r, mine);
+#else
+        if constexpr (SPLIT > 1) {
+#pragma unroll
+            for (u32 i = 0; i < 4; i++) part[(wave * 16 + 4 * fq + i) * 16 + fr] = acc[0][i];
+            __syncthreads();
+            if (sp == 0) {
+#pragma unroll
+                for (u32 i = 0; i < 4; i++) {
+                    float s = 0.0f;
+#pragma unroll
+                    for (u32 q = 0; q < SPLIT; q++) s += part[((gi * SPLIT + q) * 16 + 4 * fq + i) * 16 + fr];
+                    acc[0][i] = s;
+                }
+            }
+        }
+        if (sp == 0 && fr < m) {
+#pragma unroll
+            for (u32 i = 0; i < 4; i++) {
+                const u32 nn = n0 + 4 * fq + i;
+                if (nn < N) store_out(y, (u64)fr * N + nn, acc[0][i]);
+            }
+        }
+#endif
+        if constexpr (SPLIT > 1) __syncthreads();  // part[] reused by the next block
+    }
+}

@@ -1,0 +1,275 @@
+// moe.hip -- the MoE layer's kernels around the grouped expert GEMM: the
+// route, the sort of (row, slot) pairs by expert and its tile table, the
+// gather of X rows in sorted order, the SwiGLU over [gate | up] rows and the
+// weighted combine back to tokens.  HB_OP selects one:
+//   1 route   (src/metal/qwen_kernels.rs:1802-1884, route_qwen)
+//   2 sort    (src/metal/prefill.rs:1315-1448, moe_sort: pairs of an expert
+//             in increasing pair order)
+//   3 sort_atomic (src/metal/prefill.rs:1450-1531: any order within an expert)
+//   4 gather  (src/metal/prefill.rs:579-610, moe_gather)
+//   5 swiglu  (src/metal/qwen_kernels.rs:2087-2117, swiglu_slots)
+//   6 combine (src/metal/qwen_kernels.rs:2119-2165, moe_combine)
+// Constants: HB_OP, HB_E (experts), HB_TOPK, HB_BM (rows per expert tile),
+// HB_TILES (table capacity), HB_D (row width: hidden, or n of SwiGLU).
+#include "hb_common.h"
+
+constexpr u32 E = HB_E, TOPK = HB_TOPK, D = HB_D;
+
+#if HB_OP == 1
+// ---- route: one wavefront per row, E/64 experts per lane ----
+// p = softmax in f32 of the bf16 scores: max, e = exp(s - max), the sum in
+// the halving-tree order over the expert index (v[i] += v[i + h] for h =
+// E/2, ..., 1: first within the lane, then across lanes by xor shuffles,
+// whose lane-0 value is that tree), p = e / sum.  Top-k by repeated argmax,
+// the lowest expert on a tie; the k weights divided by their sum (added from
+// the best down), rounded to bf16, written in increasing expert order:
+// route[r][s] = expert, route[r][k + s] = the f32 bits of the bf16 weight.
+static_assert(E % 64 == 0 && E <= 1024 && TOPK <= 64, "route: experts a multiple of 64");
+constexpr u32 P = E / 64;
+
+extern "C" __global__ __launch_bounds__(256) void hb_kernel(const u16* __restrict__ scores,
+                                                            u32* __restrict__ route, u32 rows) {
+    const u32 lane = threadIdx.x & 63u;
+    const u32 r = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (r >= rows) return;
+    const u16* s = scores + (u64)r * E;
+    float v[P];
+#pragma unroll
+    for (u32 p = 0; p < P; p++) v[p] = bf16_to_f32(s[lane + 64 * p]);
+    float mx = v[0];
+#pragma unroll
+    for (u32 p = 1; p < P; p++) mx = v[p] > mx ? v[p] : mx;
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh >>= 1) {
+        float o = __shfl_xor(mx, sh, 64);
+        mx = o > mx ? o : mx;
+    }
+    float e[P], t[P];
+#pragma unroll
+    for (u32 p = 0; p < P; p++) e[p] = t[p] = hb_expf(v[p] - mx);
+#pragma unroll
+    for (u32 h = P / 2; h >= 1; h /= 2)
+#pragma unroll
+        for (u32 p = 0; p < h; p++) t[p] = t[p] + t[p + h];
+    float sum = t[0];
+#pragma unroll
+    for (int sh = 32; sh >= 1; sh >>= 1) sum = sum + __shfl_xor(sum, sh, 64);
+    sum = __shfl(sum, 0, 64);  // lane 0 holds the tree's value
+    float pr[P];
+#pragma unroll
+    for (u32 p = 0; p < P; p++) pr[p] = e[p] / sum;
+
+    u32 chosen[TOPK];
+    float vals[TOPK];
+#pragma unroll
+    for (u32 i = 0; i < TOPK; i++) {
+        float best = -2.0f;
+        u32 idx = 0;
+#pragma unroll
+        for (u32 p = 0; p < P; p++)
+            if (pr[p] > best) { best = pr[p]; idx = lane + 64 * p; }
+#pragma unroll
+        for (int sh = 32; sh >= 1; sh >>= 1) {
+            float ob = __shfl_xor(best, sh, 64);
+            u32 oi = __shfl_xor(idx, sh, 64);
+            if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
+        }
+        chosen[i] = idx;
+        vals[i] = best;
+#pragma unroll
+        for (u32 p = 0; p < P; p++)
+            if (lane + 64 * p == idx) pr[p] = -1.0f;
+    }
+    float total = 0.0f;
+#pragma unroll
+    for (u32 i = 0; i < TOPK; i++) total = total + vals[i];
+    if (lane < TOPK) {
+        u32 mine = 0;
+        float wv = 0.0f;
+#pragma unroll
+        for (u32 i = 0; i < TOPK; i++)
+            if (i == lane) { mine = chosen[i]; wv = vals[i]; }
+        u32 rank = 0;
+#pragma unroll
+        for (u32 j = 0; j < TOPK; j++) rank += chosen[j] < mine ? 1u : 0u;
+        const float w = round_bf16(wv / total);
+        u32* o = route + (u64)r * 2 * TOPK;
+        o[rank] = mine;
+        o[TOPK + rank] = __builtin_bit_cast(u32, w);
+    }
+}
+
+#elif HB_OP == 2 || HB_OP == 3
+// ---- sort: one workgroup of 1024 threads (16 wavefronts) ----
+// list[p] = pair row*TOPK + slot grouped by expert, experts ascending;
+// tiles[0] = tile count, tile t = tiles[1+3t..] = (expert, first sorted
+// row, rows <= BM).  Rows = state[3], at most the launch's m.
+static_assert(E <= 1024, "sort: at most 1024 experts");
+constexpr u32 BM = HB_BM, NW = 16;
+
+extern "C" __global__ __launch_bounds__(1024) void hb_kernel(const u32* __restrict__ state,
+                                                             const u32* __restrict__ route,
+                                                             u32* __restrict__ list,
+                                                             u32* __restrict__ tiles, u32 m_launch) {
+    __shared__ u32 hist[NW][E];  // per wave per expert: count, then the wave's cursor
+    __shared__ u32 start[E], tstart[E + 1], cnt[E];
+    const u32 tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
+    const u32 m = rows_of_state(state, m_launch);
+    const u32 pairs = m * TOPK;
+    auto expert_of = [&](u32 i) -> u32 {
+        u32 x = route[(i / TOPK) * 2 * TOPK + i % TOPK];
+        return x < E ? x : E - 1;
+    };
+    for (u32 i = tid; i < NW * E; i += 1024) (&hist[0][0])[i] = 0;
+    __syncthreads();
+#if HB_OP == 2
+    // Wave w owns pairs [w*cp, (w+1)*cp): its histogram.
+    const u32 cp = (pairs + NW - 1) / NW;
+    const u32 lo = w * cp, hi = lo + cp < pairs ? lo + cp : pairs;
+    for (u32 i = lo + lane; i < hi; i += 64) atomicAdd(&hist[w][expert_of(i)], 1u);
+#else
+    for (u32 i = tid; i < pairs; i += 1024) atomicAdd(&hist[0][expert_of(i)], 1u);
+#endif
+    __syncthreads();
+    // Per expert: its count, and each wave's offset inside the expert.
+    for (u32 x = tid; x < E; x += 1024) {
+        u32 s = 0;
+        for (u32 q = 0; q < NW; q++) {
+            u32 c = hist[q][x];
+            hist[q][x] = s;
+            s += c;
+        }
+        cnt[x] = s;
+    }
+    __syncthreads();
+    // Expert starts and tile starts (exclusive scans, in expert order).
+    if (tid == 0) {
+        u32 tot = 0, nt = 0;
+        for (u32 x = 0; x < E; x++) {
+            start[x] = tot;
+            tstart[x] = nt;
+            tot += cnt[x];
+            nt += (cnt[x] + BM - 1) / BM;
+        }
+        tstart[E] = nt;
+        tiles[0] = nt;
+    }
+    __syncthreads();
+    for (u32 x = tid; x < E; x += 1024) {
+        const u32 c = cnt[x], t0 = tstart[x];
+        for (u32 j = 0; j * BM < c; j++) {
+            u32* t = tiles + 1 + 3 * (t0 + j);
+            t[0] = x;
+            t[1] = start[x] + j * BM;
+            t[2] = c - j * BM < BM ? c - j * BM : BM;
+        }
+#pragma unroll 1
+        for (u32 q = 0; q < NW; q++) hist[q][x] += start[x];
+    }
+    __syncthreads();
+#if HB_OP == 2
+    // Place the wave's pairs chunk by chunk: a lane's rank among the earlier
+    // lanes of the same expert (ballots over the expert's bits).
+    for (u32 base = lo; base < hi; base += 64) {
+        const u32 i = base + lane;
+        const bool on = i < hi;
+        const u32 x = on ? expert_of(i) : E;  // E: matches no real expert
+        u64 same = __ballot(on);
+#pragma unroll
+        for (u32 b = 0; b < 11; b++) {
+            const u64 bal = __ballot(((x >> b) & 1u) != 0u);
+            same &= ((x >> b) & 1u) ? bal : ~bal;
+        }
+        const u64 lower = same & ((1ull << lane) - 1ull);
+        if (on) {
+            const u32 pos = hist[w][x] + (u32)__popcll(lower);
+            list[pos] = i;
+        }
+        // The group's first lane advances the wave's cursor after every
+        // lane has read it.
+        __builtin_amdgcn_s_waitcnt(0);
+        __builtin_amdgcn_wave_barrier();
+        if (on && lower == 0) hist[w][x] += (u32)__popcll(same);
+        __builtin_amdgcn_s_waitcnt(0);
+        __builtin_amdgcn_wave_barrier();
+    }
+#else
+    for (u32 i = tid; i < pairs; i += 1024) {
+        const u32 x = expert_of(i);
+        list[atomicAdd(&hist[0][x], 1u)] = i;
+    }
+#endif
+}
+
+#elif HB_OP == 4
+// ---- gather: XS[p] = X[list[p] / TOPK], 16 bytes per thread ----
+static_assert(D % 8 == 0, "gather: hidden a multiple of 8");
+constexpr u32 CELLS = D / 8;
+
+extern "C" __global__ __launch_bounds__(256) void hb_kernel(const u32* __restrict__ state,
+                                                            const u32* __restrict__ list,
+                                                            const u32x4* __restrict__ X,
+                                                            u32x4* __restrict__ XS, u32 m_launch) {
+    const u32 m = rows_of_state(state, m_launch);
+    const u64 total = (u64)m * TOPK * CELLS;
+    const u64 i = (u64)blockIdx.x * 256 + threadIdx.x;
+    if (i >= total) return;
+    const u32 p = (u32)(i / CELLS), c = (u32)(i % CELLS);
+    u32 row = list[p] / TOPK;
+    row = row < m ? row : m - 1;
+    XS[i] = X[(u64)row * CELLS + c];
+}
+
+#elif HB_OP == 5
+// ---- SwiGLU over rows of [gate (D) | up (D)]: h = rne(g * sigmoid(g) * u) ----
+static_assert(D % 8 == 0, "swiglu: n a multiple of 8");
+constexpr u32 CELLS = D / 8;
+
+extern "C" __global__ __launch_bounds__(256) void hb_kernel(const u32x4* __restrict__ gu,
+                                                            u32x4* __restrict__ h, u32 rows) {
+    const u64 i = (u64)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (u64)rows * CELLS) return;
+    const u32 s = (u32)(i / CELLS), c = (u32)(i % CELLS);
+    const u32x4 g = gu[(u64)s * 2 * CELLS + c], u = gu[(u64)s * 2 * CELLS + CELLS + c];
+    u32x4 o;
+#pragma unroll
+    for (u32 e = 0; e < 4; e++) {
+        const float g0 = bf16_lo(g[e]), g1 = bf16_hi(g[e]);
+        const float u0 = bf16_lo(u[e]), u1 = bf16_hi(u[e]);
+        const float h0 = (g0 * hb_sigmoid(g0)) * u0;
+        const float h1 = (g1 * hb_sigmoid(g1)) * u1;
+        o[e] = pack_bf16x2(h0, h1);
+    }
+    h[i] = o;
+}
+
+#elif HB_OP == 6
+// ---- combine: out[r] = the slots added in route order, each rounding as
+// index_add_ into a bf16 zero vector: acc = rne(acc + rne(y * w)) ----
+static_assert(D % 8 == 0, "combine: hidden a multiple of 8");
+constexpr u32 CELLS = D / 8;
+
+extern "C" __global__ __launch_bounds__(256) void hb_kernel(const u32x4* __restrict__ y,
+                                                            const u32* __restrict__ route,
+                                                            u32x4* __restrict__ out, u32 rows) {
+    const u64 i = (u64)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (u64)rows * CELLS) return;
+    const u32 r = (u32)(i / CELLS), c = (u32)(i % CELLS);
+    float acc[8];
+#pragma unroll
+    for (u32 e = 0; e < 8; e++) acc[e] = 0.0f;
+    for (u32 s = 0; s < TOPK; s++) {
+        const u32x4 v = y[((u64)r * TOPK + s) * CELLS + c];
+        const float w = __builtin_bit_cast(float, route[(u64)r * 2 * TOPK + TOPK + s]);
+#pragma unroll
+        for (u32 e = 0; e < 4; e++) {
+            acc[2 * e] = round_bf16(acc[2 * e] + round_bf16(bf16_lo(v[e]) * w));
+            acc[2 * e + 1] = round_bf16(acc[2 * e + 1] + round_bf16(bf16_hi(v[e]) * w));
+        }
+    }
+    u32x4 o;
+#pragma unroll
+    for (u32 e = 0; e < 4; e++) o[e] = pack_bf16x2(acc[2 * e], acc[2 * e + 1]);
+    out[i] = o;
+}
+#endif

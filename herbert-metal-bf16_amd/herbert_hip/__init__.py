@@ -93,12 +93,12 @@ class Range(ctypes.Structure):
 
 _DESC_FIELDS = ["kind", "k", "n", "out", "rows_of", "m_first", "bm", "bn", "bk", "wm", "wn",
                 "mfma", "dbuf", "swz", "order", "mv_m", "split", "persist", "rows", "form",
-                "top_k", "experts", "tiles", "rows_max"]
+                "top_k", "experts", "tiles", "rows_max", "lds_dma", "unroll"]
 
 
 class Desc(ctypes.Structure):
     """hb_desc: a kernel's shape-keyed descriptor (what an emitter fixes)."""
-    _fields_ = [(f, ctypes.c_uint32) for f in _DESC_FIELDS] + [("reserved", ctypes.c_uint32 * 8)]
+    _fields_ = [(f, ctypes.c_uint32) for f in _DESC_FIELDS] + [("reserved", ctypes.c_uint32 * 6)]
 
     def __init__(self, **kw):
         super().__init__()
@@ -227,6 +227,13 @@ def gemm_mma_rows(kdim, n, out, m_first=True, rows_of=Rows.Dense, top_k=0, tiles
 def gemm_mma(kdim, n, out, m_first=True, **tile):
     """gemm_mma (prefill.rs:418): the dense MFMA GEMM."""
     return gemm_mma_rows(kdim, n, out, m_first, Rows.Dense, **tile)
+
+
+def matvec(kdim, n, out, mv_m=1, rows=4, split=1, persist=0, form=0, unroll=4):
+    """matvec / matvec_split (kernels.rs:146, 502): y[m][n] = x[m][k].W^T for m <= mv_m;
+    form 0 the VALU layout (rows per wave), 1 the MFMA layout (16 rows per wave)."""
+    return Desc(kind=Kind.MATVEC, k=kdim, n=n, out=out, mv_m=mv_m, rows=rows, split=split,
+                persist=persist, form=form, unroll=unroll)
 
 
 class Gpu:

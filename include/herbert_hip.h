@@ -97,8 +97,9 @@ typedef struct hb_desc {
     uint32_t rows_of; /* enum hb_rows (GEMM kinds) */
     uint32_t m_first; /* tile_of (prefill.rs:31-43): walk row tiles first */
     /* GEMM tile: bm rows of X x bn rows of W per workgroup, K by bk,
-     * wm x wn wavefronts, MFMA block 16 or 32, two LDS stages, LDS swizzle
-     * shift, tile order (0 plain, 1 XCD-contiguous). 0 = the kind's default. */
+     * wm x wn wavefronts, MFMA block 16 or 32, dbuf = LDS stages - 1 (0..3),
+     * LDS swizzle (0 = conflict-free for the K step, s + 1 = shift s), tile
+     * order (0 plain, 1 XCD-contiguous). 0 = the kind's default. */
     uint32_t bm, bn, bk, wm, wn, mfma, dbuf, swz, order;
     /* matvec: rows of x (1..16), waves sharing a row block's K (split),
      * persistent workgroups (0 = one per row block), W rows per wave
@@ -107,7 +108,13 @@ typedef struct hb_desc {
     /* MoE: slots per row (top_k), experts, the tile table's capacity
      * (moe_tiles, prefill.rs:832-835), rows of the largest block. */
     uint32_t top_k, experts, tiles, rows_max;
-    uint32_t reserved[8];
+    /* GEMM staging: 0 through registers (global_load + ds_write), 1 straight
+     * into LDS (gfx950 global_load_lds_dwordx4). */
+    uint32_t lds_dma;
+    /* matvec: 16-byte chunks (VALU form) or 32-K MFMA steps (MFMA form)
+     * each lane keeps in flight per row; 0 = 4. */
+    uint32_t unroll;
+    uint32_t reserved[6];
 } hb_desc;
 
 /* Gpu::pipeline(&Emitted) (metal/gpu.rs:127-148) for the kernel the

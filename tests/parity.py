@@ -30,21 +30,28 @@ def gamma(k):
 
 def abs_products(x, w, rows=None):
     """sum_k |x_k w_k| per output, in float64 (rows: the X rows to use)."""
-    xf = np.abs(bf16_to_f32(x).astype(np.float64))
-    wf = np.abs(bf16_to_f32(w).astype(np.float64))
     if rows is not None:
-        xf = xf[rows]
-    return xf @ wf.T
+        x = x[rows]
+    xf = np.abs(bf16_to_f32(x).astype(np.float64))
+    out = np.empty((x.shape[0], w.shape[0]), np.float64)
+    step = 8192  # W by row chunks: a full lm_head in f64 would not fit
+    for c in range(0, w.shape[0], step):
+        out[:, c:c + step] = xf @ np.abs(bf16_to_f32(w[c:c + step]).astype(np.float64)).T
+    return out
 
 
-def check_close(got, want, k, absprod, what="", ulps=2.0):
-    """Asserts the contract; returns a dict of statistics for the report."""
+def check_close(got, want, k, absprod, what="", ulps=2.0, acc=None):
+    """Asserts the contract; returns a dict of statistics for the report.
+    acc: Out::Residual's f32 sums (y = rne(y + rne(acc)) rounds twice: one
+    bf16 ulp of rne(acc) joins the bound)."""
     g = bf16_to_f32(got).astype(np.float64) if got.dtype == np.uint16 else got.astype(np.float64)
     t = bf16_to_f32(want).astype(np.float64) if want.dtype == np.uint16 else want.astype(np.float64)
     assert g.shape == t.shape, (g.shape, t.shape)
     assert np.all(np.isfinite(g)), what + ": non-finite outputs"
     err = np.abs(g - t)
     bound = ulps * bf16_ulp(np.maximum(np.abs(g), np.abs(t))) + 2 * gamma(k) * absprod
+    if acc is not None:
+        bound = bound + bf16_ulp(np.abs(np.asarray(acc, np.float64)))
     bad = err > bound
     scale = max(np.abs(t).max(), 1e-6)
     stats = {

@@ -1,0 +1,165 @@
+"""Parity of the HIP prefill GEMM (gemm_mma_rows, prefill.rs:838-1307) with
+the CPU oracle: every Out mode, partial row tiles, every tile family the
+autotuner can pick, the BASELINE configs (rows sampled for the oracle), and
+size-independent properties at full size."""
+import numpy as np
+import pytest
+
+import herbert_hip as hb
+import hb_oracle as orc
+from parity import abs_products, bf16_to_f32, check_close
+
+pytestmark = pytest.mark.gpu
+
+# The tile families of the candidate list (bm, bn, bk, wm, wn, mfma, stages, dma).
+TILES = {
+    "t128x128_x16_d2": dict(bm=128, bn=128, bk=64, wm=2, wn=2, mfma=16, dbuf=1, lds_dma=1, order=1),
+    "t128x128_x32_d2": dict(bm=128, bn=128, bk=64, wm=2, wn=2, mfma=32, dbuf=1, lds_dma=1, order=1),
+    "t256x256_x32_d2": dict(bm=256, bn=256, bk=64, wm=2, wn=2, mfma=32, dbuf=1, lds_dma=1, order=1),
+    "t256x256_w8_d4": dict(bm=256, bn=256, bk=32, wm=4, wn=2, mfma=32, dbuf=3, lds_dma=1, order=1),
+    "t256x128_d4": dict(bm=128, bn=256, bk=32, wm=2, wn=2, mfma=32, dbuf=3, lds_dma=1, order=1),
+    "t128x128_reg_d1": dict(bm=128, bn=128, bk=64, wm=2, wn=2, mfma=16, dbuf=1, lds_dma=0, order=0),
+    "t64x64_reg_s1": dict(bm=64, bn=64, bk=32, wm=1, wn=4, mfma=16, dbuf=0, lds_dma=0, order=0),
+}
+
+
+def run_gemm(gpu, x, w, out=0, y0=None, m=None, **tile):
+    m_rows, k = x.shape
+    n = w.shape[0]
+    m = m_rows if m is None else m
+    st = gpu.alloc_with(np.array([0, 0, 0, m], np.uint32))
+    W = gpu.alloc_with(w)
+    X = gpu.alloc_with(x)
+    esz = 4 if out == 1 else 2
+    Y = gpu.alloc_with(y0) if y0 is not None else gpu.alloc(m_rows * n * esz)
+    try:
+        kern = gpu.pipeline(hb.gemm_mma(k, n, out, **tile))
+        gpu.launch(kern, [hb.r(st), hb.r(W), hb.r(X), hb.r(Y), hb.r(st), hb.r(st)], m)
+        gpu.sync()
+        return gpu.download(Y, np.float32 if out == 1 else np.uint16, m_rows * n).reshape(m_rows, n)
+    finally:
+        for b in (st, W, X, Y):
+            gpu.free(b)
+
+
+def inputs(m, k, n, seed):
+    return hb.normal_bf16(seed, 1.0, (m, k)), hb.normal_bf16(seed + 1, 0.02, (n, k))
+
+
+@pytest.mark.parametrize("out", [0, 1, 2])
+@pytest.mark.parametrize("tile", sorted(TILES))
+def test_gemm_config1_all_out_modes(gpu, tile, out):
+    """M=512, K=1024, N=3584, full check of every output."""
+    m, k, n = 512, 1024, 3584
+    x, w = inputs(m, k, n, 0x5EED0001)
+    y0 = hb.normal_bf16(77, 1.0, (m, n)) if out == 2 else None
+    got = run_gemm(gpu, x, w, out, y0, **TILES[tile])
+    want = orc.gemm(x, w, out, y0)
+    acc = orc.gemm(x, w, orc.OUT_F32) if out == 2 else None
+    st = check_close(got, want, k, abs_products(x, w), "config1 %s out=%d" % (tile, out), acc=acc)
+    if out != 1:
+        assert st["exact"] > 0.99, st
+
+
+@pytest.mark.parametrize("tile", sorted(TILES))
+def test_gemm_partial_tiles(gpu, tile):
+    """A row count that is a multiple of no tile (m - m/3 - 3, the reference's
+    partial check, qwen.rs:2518): rows past m are neither wrong nor written."""
+    m_alloc, k, n = 200, 512, 1024
+    m = m_alloc - m_alloc // 3 - 3
+    x, w = inputs(m_alloc, k, n, 11)
+    sentinel = np.full((m_alloc, n), 0x7FC1, np.uint16)
+    got = run_gemm(gpu, x, w, 0, sentinel, m=m, **TILES[tile])
+    want = orc.gemm(x[:m], w)
+    check_close(got[:m], want, k, abs_products(x[:m], w), "partial " + tile)
+    assert np.all(got[m:] == 0x7FC1), "rows past m were written"
+
+
+def test_gemm_state_rows_below_launch_rows(gpu):
+    """state[3] < the launch's m: the kernel does only state[3] rows."""
+    m, k, n = 256, 256, 512
+    x, w = inputs(m, k, n, 12)
+    st = gpu.alloc_with(np.array([0, 0, 0, 100], np.uint32))
+    W, X = gpu.alloc_with(w), gpu.alloc_with(x)
+    Y = gpu.alloc_with(np.zeros((m, n), np.uint16))
+    kern = gpu.pipeline(hb.gemm_mma(k, n, 0, **TILES["t128x128_x16_d2"]))
+    gpu.launch(kern, [hb.r(st), hb.r(W), hb.r(X), hb.r(Y), hb.r(st), hb.r(st)], m)
+    got = gpu.download(Y, np.uint16, m * n).reshape(m, n)
+    for b in (st, W, X, Y):
+        gpu.free(b)
+    assert np.all(got[100:] == 0)
+    check_close(got[:100], orc.gemm(x[:100], w), k, abs_products(x[:100], w), "state rows")
+
+
+LAYER4B = [("qkv", 2560, 4608, 0), ("o", 4096, 2560, 2), ("gate_up", 2560, 18432, 0),
+           ("down", 9216, 2560, 2)]
+
+
+@pytest.mark.parametrize("m", [512, 2048])
+@pytest.mark.parametrize("name,k,n,out", LAYER4B)
+def test_gemm_config2_layer_shapes(gpu, name, k, n, out, m):
+    """BASELINE config 2 (4B-class layer) at M=512 and 2048: 48 rows sampled
+    across the block (first, last, spread) against the oracle."""
+    tile = TILES["t128x128_x16_d2"] if m == 512 else TILES["t256x256_w8_d4"]
+    x, w = inputs(m, k, n, 0x5EED0002)
+    y0 = hb.normal_bf16(5, 1.0, (m, n)) if out == 2 else None
+    got = run_gemm(gpu, x, w, out, y0, **tile)
+    rows = np.unique(np.concatenate([[0, 1, m - 1], np.linspace(0, m - 1, 45).astype(int)]))
+    want = orc.gemm(x[rows], w, out, None if y0 is None else y0[rows])
+    acc = orc.gemm(x[rows], w, orc.OUT_F32) if out == 2 else None
+    check_close(got[rows], want, k, abs_products(x, w, rows), "%s m=%d" % (name, m), acc=acc)
+
+
+@pytest.mark.parametrize("name,k,n", [("qkv", 5120, 7168), ("gate_up", 5120, 34816),
+                                      ("down", 17408, 5120), ("lm_head", 5120, 151936)])
+def test_gemm_config4_27b_shapes(gpu, name, k, n):
+    """BASELINE config 4 (27B-class) at M=2048, 8 rows sampled."""
+    m = 2048
+    x, w = inputs(m, k, n, 0x5EED0004)
+    got = run_gemm(gpu, x, w, 0, **TILES["t256x256_w8_d4"])
+    rows = np.array([0, 1, 517, 1024, 1500, 2000, 2046, 2047])
+    want = orc.gemm(x[rows], w)
+    check_close(got[rows], want, k, abs_products(x, w, rows), name)
+
+
+def test_gemm_full_size_properties(gpu):
+    """Size-independent invariants at M=2048 on the gate|up shape: scaling W
+    by 2 scales Y exactly; permuting X's rows permutes Y's rows exactly;
+    every tile family gives outputs within the contract of each other."""
+    m, k, n = 2048, 2560, 18432
+    x, w = inputs(m, k, n, 21)
+    tile = TILES["t256x256_w8_d4"]
+    y = run_gemm(gpu, x, w, 0, **tile)
+    w2 = hb.f32_to_bf16(bf16_to_f32(w) * 2)
+    y2 = run_gemm(gpu, x, w2, 0, **tile)
+    assert np.array_equal(bf16_to_f32(y2), bf16_to_f32(y) * 2)
+    perm = np.random.default_rng(0).permutation(m)
+    yp = run_gemm(gpu, x[perm], w, 0, **tile)
+    assert np.array_equal(yp, y[perm])
+    other = run_gemm(gpu, x, w, 0, **TILES["t128x128_x16_d2"])
+    scale = np.abs(bf16_to_f32(y)).max()
+    assert np.abs(bf16_to_f32(other) - bf16_to_f32(y)).max() <= scale / 64
+
+
+def test_gemm_identity_is_exact(gpu):
+    m, k = 384, 512
+    x = hb.normal_bf16(3, 1.0, (m, k))
+    eye = hb.f32_to_bf16(np.eye(k, dtype=np.float32))
+    for tile in ("t128x128_x16_d2", "t256x256_x32_d2"):
+        assert np.array_equal(run_gemm(gpu, x, eye, 0, **TILES[tile]), x)
+
+
+def test_gemm_bindings_checked(gpu):
+    """A binding smaller than the descriptor and m need is refused before
+    anything runs (HerbertError, no launch)."""
+    k, n, m = 256, 512, 64
+    kern = gpu.pipeline(hb.gemm_mma(k, n, 0, **TILES["t128x128_x16_d2"]))
+    st = gpu.alloc_with(np.array([0, 0, 0, m], np.uint32))
+    W = gpu.alloc(n * k * 2)
+    X = gpu.alloc(m * k * 2 - 2)
+    Y = gpu.alloc(m * n * 2)
+    with pytest.raises(hb.HerbertError) as e:
+        gpu.launch(kern, [hb.r(st), hb.r(W), hb.r(X), hb.r(Y), hb.r(st), hb.r(st)], m)
+    assert "X" in str(e.value)
+    for b in (st, W, X, Y):
+        gpu.free(b)

@@ -1,0 +1,301 @@
+"""CPU checks that pin the oracle (oracle/hb_oracle.c) to the reference's
+contract independently of its own code: the reference's branchy RNE over
+every f32 pattern, exact-sum GEMM cases, identity / permutation / scaling
+invariants, float32 scalar restatements of the summation order, and numpy
+restatements of the route, sort, SwiGLU and combine."""
+import math
+import struct
+
+import numpy as np
+import pytest
+
+import hb_oracle as orc
+from parity import bf16_to_f32
+
+
+def rne_branchy(bits):
+    """src/core/bf16.rs:13-23 as written there: round bit and sticky bits."""
+    bits = bits.astype(np.uint32)
+    lsb = (bits >> np.uint32(16)) & np.uint32(1)
+    rnd = (bits >> np.uint32(15)) & np.uint32(1)
+    sticky = bits & np.uint32(0x7FFF)
+    res = bits >> np.uint32(16)
+    up = (rnd == 1) & ((sticky != 0) | (lsb == 1))
+    return (res + up.astype(np.uint32)).astype(np.uint16)
+
+
+def test_rne_exhaustive_all_f32_patterns():
+    """Every one of the 2^32 f32 bit patterns (bf16.rs:13-23), as the
+    reference's own `herbert-metal-probe round` checks its GPU text."""
+    chunk = 1 << 24
+    out = np.empty(chunk, np.uint16)
+    base = np.arange(chunk, dtype=np.uint32)
+    bits = np.empty(chunk, np.uint32)
+    t = np.empty(chunk, np.uint32)
+    up = np.empty(chunk, np.uint32)
+    for c in range(1 << 32 >> 24):
+        first = c * chunk
+        orc.lib.hbo_f32_to_bf16_range(first, chunk, out.ctypes.data_as(orc._P))
+        np.add(base, np.uint32(first), out=bits)
+        # branchy form: up = round_bit & (sticky != 0 | lsb)
+        np.bitwise_and(bits, np.uint32(0x7FFF), out=t)
+        np.not_equal(t, 0, out=up, casting="unsafe")
+        np.right_shift(bits, np.uint32(16), out=t)
+        np.bitwise_and(t, np.uint32(1), out=t)
+        np.bitwise_or(up, t, out=up)
+        np.right_shift(bits, np.uint32(15), out=t)
+        np.bitwise_and(up, t, out=up)
+        np.bitwise_and(up, np.uint32(1), out=up)
+        np.right_shift(bits, np.uint32(16), out=t)
+        np.add(t, up, out=t)
+        if not np.array_equal(out, t.astype(np.uint16)):
+            want = t.astype(np.uint16)
+            i = int(np.argmax(out != want))
+            raise AssertionError("pattern %#010x: %#06x vs %#06x" % (first + i, out[i], want[i]))
+
+
+def test_rne_special_values():
+    f = orc.lib.hbo_f32_to_bf16
+    assert f(0.0) == 0x0000 and f(-0.0) == 0x8000
+    assert f(float("inf")) == 0x7F80 and f(float("-inf")) == 0xFF80
+    assert f(1.0) == 0x3F80
+    # ties to even: 1 + 2^-8 is halfway between 1 and 1 + 2^-7 -> 1
+    assert f(1.0 + 2.0 ** -8) == 0x3F80
+    assert f(1.0 + 3 * 2.0 ** -8) == 0x3F82  # halfway, odd below -> up
+    # the largest finite f32 rounds to infinity
+    assert f(struct.unpack("<f", struct.pack("<I", 0x7F7FFFFF))[0]) == 0x7F80
+    for h in (0x0001, 0x3F80, 0x7F7F, 0x8001, 0xC2F7):
+        assert orc.lib.hbo_f32_to_bf16(orc.lib.hbo_bf16_to_f32(h)) == h
+
+
+def _exact_inputs(rng, shape, emin, emax, mbits):
+    """bf16 values with few mantissa bits and a narrow exponent range, so that
+    every product and partial sum below is exact in f32 and f64 alike."""
+    sign = rng.integers(0, 2, shape) * 2 - 1
+    e = rng.integers(emin, emax + 1, shape).astype(np.float64)
+    m = rng.integers(0, 1 << mbits, shape).astype(np.float64)
+    v = sign * (1 + m / (1 << mbits)) * 2.0 ** e
+    return orc_f32_to_bf16(v)
+
+
+def orc_f32_to_bf16(a):
+    b = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+    return rne_branchy(b)
+
+
+@pytest.mark.parametrize("k", [1, 2, 8, 64])
+def test_gemm_exact_sums_match_f64(k):
+    """Small K with short mantissas: every summation order is exact, so the
+    oracle must equal rne of the f64 dot product."""
+    rng = np.random.default_rng(k)
+    m, n = 7, 13
+    x = _exact_inputs(rng, (m, k), -2, 2, 3)
+    w = _exact_inputs(rng, (n, k), -2, 2, 3)
+    want64 = bf16_to_f32(x).astype(np.float64) @ bf16_to_f32(w).astype(np.float64).T
+    got = orc.gemm(x, w, orc.OUT_F32)
+    assert np.array_equal(got.astype(np.float64), want64)
+    got16 = orc.gemm(x, w, orc.OUT_BF16)
+    assert np.array_equal(got16, orc_f32_to_bf16(want64))
+
+
+def test_gemm_identity_and_permutation():
+    rng = np.random.default_rng(1)
+    m, k = 9, 48
+    x = orc_f32_to_bf16(rng.standard_normal((m, k)))
+    eye = orc_f32_to_bf16(np.eye(k))
+    assert np.array_equal(orc.gemm(x, eye), x)
+    perm = rng.permutation(k)
+    assert np.array_equal(orc.gemm(x, eye[perm]), x[:, perm])
+    # Residual: y = rne(y + rne(acc)); with acc = x exactly.
+    y0 = orc_f32_to_bf16(rng.standard_normal((m, k)))
+    want = orc_f32_to_bf16(bf16_to_f32(y0) + bf16_to_f32(x))
+    assert np.array_equal(orc.gemm(x, eye, orc.OUT_RESIDUAL, y=y0), want)
+
+
+def test_gemm_power_of_two_scaling_is_exact():
+    rng = np.random.default_rng(2)
+    x = orc_f32_to_bf16(rng.standard_normal((5, 256)))
+    w = orc_f32_to_bf16(rng.standard_normal((11, 256)) * 0.02)
+    y = orc.gemm(x, w, orc.OUT_F32)
+    y4 = orc.gemm(x, orc_f32_to_bf16(bf16_to_f32(w) * 4), orc.OUT_F32)
+    assert np.array_equal(y4, y * 4)
+
+
+def test_gemm_sums_in_increasing_k_order():
+    """The contract's order: f32 adds in increasing k (a float32 scalar loop
+    in numpy, not the oracle's C), visible under cancellation."""
+    rng = np.random.default_rng(3)
+    k = 97
+    x = orc_f32_to_bf16(rng.standard_normal((3, k)) * np.float32(1e3) ** rng.integers(0, 2, (3, k)))
+    w = orc_f32_to_bf16(rng.standard_normal((4, k)))
+    got = orc.gemm(x, w, orc.OUT_F32)
+    xf, wf = bf16_to_f32(x), bf16_to_f32(w)
+    for i in range(3):
+        for j in range(4):
+            acc = np.float32(0)
+            for t in range(k):
+                acc = np.float32(acc + np.float32(xf[i, t] * wf[j, t]))
+            assert got[i, j] == acc
+    # and the order matters here: the reversed order differs somewhere
+    rev = [[np.float32(0)] * 4 for _ in range(3)]
+    for i in range(3):
+        for j in range(4):
+            acc = np.float32(0)
+            for t in reversed(range(k)):
+                acc = np.float32(acc + np.float32(xf[i, t] * wf[j, t]))
+            rev[i][j] = acc
+    assert not np.array_equal(np.array(rev, np.float32), got)
+
+
+def test_threads_do_not_change_bits():
+    rng = np.random.default_rng(4)
+    x = orc_f32_to_bf16(rng.standard_normal((33, 200)))
+    w = orc_f32_to_bf16(rng.standard_normal((70, 200)) * 0.02)
+    assert np.array_equal(orc.gemm(x, w, threads=1), orc.gemm(x, w, threads=7))
+
+
+def test_expf_within_two_ulp_of_libm():
+    xs = np.concatenate([np.linspace(-100, 88, 200001), np.linspace(-1, 1, 20001),
+                         [0.0, -0.0, 1e-30, -1e-30, 88.5, -87.0]]).astype(np.float32)
+    for x in xs[::7]:
+        got = orc.expf(float(x))
+        want = math.exp(float(x))
+        if want < 1.2e-38:  # subnormal results: absolute bound
+            assert abs(got - want) <= 2 * 2.0 ** -149
+            continue
+        ulp = 2.0 ** (math.floor(math.log2(want)) - 23)
+        assert abs(got - want) <= 2 * ulp, (x, got, want)
+    assert orc.expf(float("inf")) == float("inf") and orc.expf(-1000.0) == 0.0
+
+
+def np_expf(x):
+    return np.array([orc.expf(float(v)) for v in np.asarray(x, np.float32).ravel()],
+                    np.float32).reshape(np.shape(x))
+
+
+def route_numpy(scores, top_k):
+    """qwen_kernels.rs:1802-1884 restated with numpy: the tie rule by a stable
+    sort on (-p, index), the sums in the documented tree / selection order."""
+    rows, experts = scores.shape
+    s = bf16_to_f32(scores)
+    out = np.zeros((rows, 2 * top_k), np.uint32)
+    for r in range(rows):
+        mx = s[r].max()
+        e = np_expf(s[r] - mx)
+        t = e.copy()
+        h = experts // 2
+        while h >= 1:
+            t[:h] = t[:h] + t[h:2 * h]
+            h //= 2
+        p = (e / t[0]).astype(np.float32)
+        order = np.lexsort((np.arange(experts), -p.astype(np.float64)))
+        chosen = order[:top_k]
+        vals = p[chosen]
+        total = np.float32(0)
+        for v in vals:
+            total = np.float32(total + v)
+        wts = orc_f32_to_bf16((vals / total).astype(np.float32))
+        idx = np.argsort(chosen, kind="stable")
+        out[r, :top_k] = chosen[idx]
+        out[r, top_k:] = (wts[idx].astype(np.uint32) << np.uint32(16))
+    return out
+
+
+def test_route_matches_numpy_restatement_with_ties():
+    rng = np.random.default_rng(5)
+    scores = orc_f32_to_bf16(rng.standard_normal((40, 256)))
+    # force exact ties in a few rows (lowest index must win)
+    scores[3, 10] = scores[3, 200] = orc_f32_to_bf16(np.float32([9.0]))[0]
+    scores[4, :] = orc_f32_to_bf16(np.float32([0.5]))[0]
+    got = orc.route(scores, 8)
+    assert np.array_equal(got, route_numpy(scores, 8))
+    assert 10 in got[3, :8] and 200 in got[3, :8]
+    assert list(got[4, :8]) == list(range(8))
+    w = bf16_to_f32((got[:, 8:] >> 16).astype(np.uint16))
+    assert np.all(np.abs(w.sum(1) - 1) < 0.05)
+
+
+def test_moe_sort_invariants():
+    rng = np.random.default_rng(6)
+    rows, top_k, experts = 300, 8, 64
+    route = np.zeros((rows, 2 * top_k), np.uint32)
+    for r in range(rows):
+        route[r, :top_k] = np.sort(rng.choice(experts, top_k, replace=False))
+    for bm in (16, 32, 64):
+        lst, tiles = orc.moe_sort(route, top_k, experts, bm)
+        pairs = rows * top_k
+        assert sorted(lst.tolist()) == list(range(pairs))
+        ex = route[lst // top_k, lst % top_k]
+        assert np.all(np.diff(ex.astype(np.int64)) >= 0)
+        for e in range(experts):
+            sel = lst[ex == e]
+            assert np.all(np.diff(sel.astype(np.int64)) > 0)
+        counts = np.bincount(ex, minlength=experts)
+        nt = int(tiles[0])
+        assert nt == int(sum(-(-c // bm) for c in counts))
+        covered = np.zeros(pairs, np.int64)
+        for t in range(nt):
+            e, start, cnt = tiles[1 + 3 * t: 4 + 3 * t]
+            assert 1 <= cnt <= bm
+            assert np.all(ex[start:start + cnt] == e)
+            covered[start:start + cnt] += 1
+        assert np.all(covered == 1)
+
+
+def test_experts_gemm_equals_dense_gemm_per_expert():
+    rng = np.random.default_rng(7)
+    rows, top_k, experts, hidden, n = 24, 4, 8, 64, 32
+    route = np.zeros((rows, 2 * top_k), np.uint32)
+    for r in range(rows):
+        route[r, :top_k] = np.sort(rng.choice(experts, top_k, replace=False))
+    x = orc_f32_to_bf16(rng.standard_normal((rows, hidden)))
+    w = orc_f32_to_bf16(rng.standard_normal((experts * n, hidden)) * 0.02)
+    lst, tiles = orc.moe_sort(route, top_k, experts, 16)
+    pairs = rows * top_k
+    gu = orc.experts_gemm(x, w, lst, tiles, hidden, n, 1, top_k, pairs)
+    for p in range(pairs):
+        pair = lst[p]
+        e = route[pair // top_k, pair % top_k]
+        want = orc.gemm(x[pair // top_k][None], w[e * n:(e + 1) * n])
+        assert np.array_equal(gu[p], want[0])
+    # Scatter: sorted row p lands at its slot row list[p].
+    xs = orc_f32_to_bf16(rng.standard_normal((pairs, n)))
+    w2 = orc_f32_to_bf16(rng.standard_normal((experts * hidden, n)) * 0.02)
+    y = orc.experts_gemm(xs, w2, lst, tiles, n, hidden, 2, top_k, pairs)
+    for p in range(0, pairs, 5):
+        pair = lst[p]
+        e = route[pair // top_k, pair % top_k]
+        want = orc.gemm(xs[p][None], w2[e * hidden:(e + 1) * hidden])
+        assert np.array_equal(y[pair], want[0])
+
+
+def test_swiglu_and_fused_swiglu():
+    rng = np.random.default_rng(8)
+    n = 48
+    gu = orc_f32_to_bf16(rng.standard_normal((10, 2 * n)) * 3)
+    h = orc.swiglu(gu, n)
+    g = bf16_to_f32(gu[:, :n])
+    u = bf16_to_f32(gu[:, n:])
+    sig = (np.float32(1) / (np.float32(1) + np_expf(-g))).astype(np.float32)
+    want = orc_f32_to_bf16(((g * sig).astype(np.float32) * u).astype(np.float32))
+    assert np.array_equal(h, want)
+    x = orc_f32_to_bf16(rng.standard_normal((6, 64)))
+    w = orc_f32_to_bf16(rng.standard_normal((2 * n, 64)) * 0.1)
+    assert np.array_equal(orc.gemm_swiglu(x, w, n), orc.swiglu(orc.gemm(x, w), n))
+
+
+def test_combine_order_and_rounding():
+    rng = np.random.default_rng(9)
+    rows, top_k, d = 7, 8, 40
+    route = np.zeros((rows, 2 * top_k), np.uint32)
+    wts = orc_f32_to_bf16(rng.random((rows, top_k)).astype(np.float32) / 4)
+    route[:, top_k:] = wts.astype(np.uint32) << np.uint32(16)
+    y = orc_f32_to_bf16(rng.standard_normal((rows * top_k, d)))
+    got = orc.combine(y, route, top_k, d)
+    yf = bf16_to_f32(y).reshape(rows, top_k, d)
+    wf = bf16_to_f32(wts)
+    acc = np.zeros((rows, d), np.float32)
+    for s in range(top_k):
+        c = bf16_to_f32(orc_f32_to_bf16((yf[:, s] * wf[:, s:s + 1]).astype(np.float32)))
+        acc = bf16_to_f32(orc_f32_to_bf16((acc + c).astype(np.float32)))
+    assert np.array_equal(got, orc_f32_to_bf16(acc))
