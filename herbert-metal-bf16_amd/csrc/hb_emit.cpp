@@ -71,7 +71,7 @@ int emit(const hb_desc& d, Emitted* e) {
             e->nbind = 1;
             return HB_OK;
         case HB_KIND_GEMM: {
-            if (d.rows_of > HB_ROWS_SCATTER || d.out > HB_OUT_RESIDUAL)
+            if (d.rows_of > HB_ROWS_SORTED || d.out > HB_OUT_RESIDUAL)
                 return fail(HB_ERR_INVALID, "gemm: rows_of/out out of range");
             if (d.mfma != 16 && d.mfma != 32) return fail(HB_ERR_UNSUPPORTED, "gemm: mfma 16 or 32");
             if (!d.k || !d.n || d.k % d.bk || d.n % 4 || !pow2(d.bk) || d.bk < 32)
@@ -99,6 +99,9 @@ int emit(const hb_desc& d, Emitted* e) {
             } else if (d.rows_of == HB_ROWS_SCATTER) {
                 snprintf(name, sizeof name, "_scatter_t%u_m%u", d.tiles, d.bm);
                 rows = name;
+            } else if (d.rows_of == HB_ROWS_SORTED) {
+                snprintf(name, sizeof name, "_sorted_k%u_t%u_m%u", d.top_k, d.tiles, d.bm);
+                rows = name;
             }
             if (d.dbuf > 3 || (!d.lds_dma && d.dbuf > 1))
                 return fail(HB_ERR_UNSUPPORTED, "gemm: stages 1..4 (1..2 through registers)");
@@ -120,6 +123,32 @@ int emit(const hb_desc& d, Emitted* e) {
                           D("HB_DMA", d.lds_dma ? 1 : 0)};
             return HB_OK;
         }
+        case HB_KIND_GEMM_SIMT:
+            if (d.rows_of != HB_ROWS_DENSE || d.out > HB_OUT_RESIDUAL || !d.k || d.k % 16 || !d.n)
+                return fail(HB_ERR_UNSUPPORTED, "gemm_simt: dense rows, K a multiple of 16");
+            snprintf(name, sizeof name, "gemm_simt_%ux%u_%s%s", d.k, d.n, out_tag(d.out),
+                     d.m_first ? "_mf" : "");
+            e->name = name;
+            e->source = "gemm_simt.hip";
+            e->threads = 256;
+            e->nbind = 6;
+            e->defines = {D("HB_K", d.k), D("HB_N", d.n), D("HB_OUT", d.out),
+                          D("HB_MFIRST", d.m_first ? 1 : 0)};
+            return HB_OK;
+        case HB_KIND_GEMM_DIRECT:
+            if (d.rows_of != HB_ROWS_DENSE || d.out > HB_OUT_RESIDUAL || !d.k || d.k % 32 ||
+                !d.n || d.n % 4 || d.bm % 16 || d.bn % 16 || !d.bm || !d.bn ||
+                (d.bm / 16) * (d.bn / 16) > 16)
+                return fail(HB_ERR_UNSUPPORTED, "gemm_mm2d: dense, K a multiple of 32, tiles of 16..64");
+            snprintf(name, sizeof name, "gemm_mm2d_%ux%u_%s%s_%ux%u", d.k, d.n, out_tag(d.out),
+                     d.m_first ? "_mf" : "", d.bm, d.bn);
+            e->name = name;
+            e->source = "gemm_direct.hip";
+            e->threads = 64 * (d.bm / 16) * (d.bn / 16);
+            e->nbind = 6;
+            e->defines = {D("HB_K", d.k), D("HB_N", d.n), D("HB_OUT", d.out), D("HB_BM", d.bm),
+                          D("HB_BN", d.bn), D("HB_MFIRST", d.m_first ? 1 : 0)};
+            return HB_OK;
         case HB_KIND_MATVEC: {
             if (d.out > HB_OUT_RESIDUAL || d.form > 1)
                 return fail(HB_ERR_INVALID, "matvec: out / form out of range");
@@ -211,9 +240,10 @@ uint32_t groups_of(const hb_desc& d, uint32_t m) {
         case HB_KIND_GEMM_DIRECT:
         case HB_KIND_GEMM_SIMT:
         case HB_KIND_GEMM_SWIGLU: {
-            uint32_t nt = cdiv(d.n, d.bn);
+            uint32_t bm = d.kind == HB_KIND_GEMM_SIMT ? 64 : d.bm;
+            uint32_t nt = cdiv(d.n, d.kind == HB_KIND_GEMM_SIMT ? 64 : d.bn);
             if (d.rows_of != HB_ROWS_DENSE) return d.tiles * nt;  // gemm_mma_expert_groups
-            return cdiv(m, d.bm) * nt;                               // gemm_mma_groups
+            return cdiv(m, bm) * nt;                                 // gemm_mma_groups
         }
         case HB_KIND_MATVEC: {  // matvec_groups / matvec_split_groups
             uint32_t rb = d.form == 1 ? 16 : d.rows, per = 4 / d.split;
@@ -259,7 +289,7 @@ int check_bindings(const hb_desc& d, const uint64_t* s, uint32_t nbind, uint32_t
         } else {
             uint64_t pairs = mm * d.top_k;
             if ((rc = need(s, 1, (uint64_t)d.experts * nw * k * 2, "W"))) return rc;
-            uint64_t xrows = d.rows_of == HB_ROWS_GATHER ? mm : pairs;
+            uint64_t xrows = d.rows_of == HB_ROWS_GATHER ? mm : pairs;  // scatter, sorted: pairs
             if ((rc = need(s, 2, xrows * k * 2, "X"))) return rc;
             if ((rc = need(s, 3, pairs * yn * out_bytes(d.out), "Y"))) return rc;
             if ((rc = need(s, 4, pairs * 4, "list"))) return rc;

@@ -49,7 +49,7 @@ extern "C" void hb_fill_normal_bf16(uint64_t seed, float std_, uint16_t* out, ui
     if (threads < 1) threads = 1;
     if (threads > 64) threads = 64;
     if (n < (1u << 16)) threads = 1;
-    uint64_t per = ((n / threads) + 1) & ~1ull;
+    uint64_t per = ((n + threads - 1) / threads + 1) & ~1ull;  // even, covers n
     std::vector<std::thread> t;
     for (int i = 0; i < threads; i++) {
         uint64_t lo = per * i, hi = lo + per < n ? lo + per : n;

@@ -1,14 +1,802 @@
-// hb_select.cpp -- placeholder until the selection layer lands.
+// hb_select.cpp -- the kernel-selection part of the reference's QwenEngine,
+// over this library's kernels: the --tune settings (Tune::apply / summary),
+// the shape-keyed GEMM choice with its candidates checked against the first
+// one and timed (gemm, check_candidates, pick_flagged), the decode matvec's
+// form (mv_full) and the MoE layer's sort / grouped GEMMs / tile rows
+// (expert_pipes), with the reference's [autotune] log lines.
+//
+// Reference: src/metal/qwen.rs:62-398 (Tune), :1051-1063 (buckets),
+// :1311-1511 (mv_full), :2200-2325 (gemm), :2326-2391 (expert_pipes),
+// :2483-2628 (pick, check_candidates, pick_flagged, heat, time_ops).
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <map>
+#include <sstream>
+
 #include "hb_internal.h"
+
 using namespace hb;
-struct hb_engine { hb_gpu* gpu; };
-extern "C" {
-int hb_engine_open(hb_gpu*, const char*, hb_engine** e) { *e = nullptr; return fail(HB_ERR_UNSUPPORTED, "engine"); }
-void hb_engine_close(hb_engine*) {}
-const char* hb_engine_tune_summary(hb_engine*) { return ""; }
-int hb_engine_buckets(hb_engine*, uint32_t*, uint32_t, uint32_t*) { return HB_ERR_UNSUPPORTED; }
-int hb_engine_gemm(hb_engine*, uint32_t, uint32_t, uint32_t, hb_range, hb_range, hb_range, hb_range, uint32_t, int32_t*) { return HB_ERR_UNSUPPORTED; }
-int hb_engine_matvec(hb_engine*, uint32_t, uint32_t, uint32_t, uint32_t, const hb_range*, uint32_t, hb_range, hb_range, int32_t*) { return HB_ERR_UNSUPPORTED; }
-int hb_engine_experts(hb_engine*, uint32_t, uint32_t, uint32_t, uint32_t, uint32_t, const hb_moe_io*, int32_t*, uint32_t*) { return HB_ERR_UNSUPPORTED; }
-double hb_engine_autotune_seconds(hb_engine*) { return 0; }
+
+namespace {
+
+// ---- Tune (qwen.rs:62-398) ----
+
+// Every key of the reference's --tune, with its default, in the order of
+// Tune::summary.  The keys of this path act (prefill.block, gemm.*, moe.*,
+// mv.*, auto.heat, pf.fswi); the others are accepted and echoed, as the
+// reference's subsystems they name (attention, DeltaNet, decode fusions, Q4)
+// are not part of this library.
+struct Key {
+    const char* name;
+    uint32_t def;
+};
+const Key kKeys[] = {
+    {"prefill.block", 2048}, {"rec.chunk", 3},   {"rec.pcols", 16},  {"rec.pslices", 16},
+    {"rec.vec", 0},          {"rec.pair", 0},    {"rec.stage", 0},   {"conv.cols", 32},
+    {"sdpa.prefill", 1},     {"sdpa.bq", 16},    {"sdpa.bk", 16},    {"sdpa.mq", 0},
+    {"sdpa.mk", 32},         {"sdpa.qreg", 0},   {"sdpa.kt", 0},     {"sdpa.msg", 8},
+    {"sdpa.auto", 1},        {"auto.heat", 0},   {"gemm.simt", 1},   {"gemm.auto", 1},
+    {"gemm.mma", 1},         {"gemm.tn", 64},    {"gemm.mform", 0},  {"gemm.half", 1},
+    {"gemm.mfirst", 1},      {"moe.grouped", 1}, {"moe.tile", 16},   {"q4.fuse", 0},
+    {"mv.auto", 1},          {"mv.masks", 0},    {"mv.split", 1},    {"mv.splitauto", 1},
+    {"mv.persist", 0},       {"mv.persists", 0}, {"dec.sdpa", 32},   {"mv.cold", 1},
+    {"dec.swiglu", 0},       {"dec.prep", 0},    {"dec.conc", 0},    {"dec.pf", 0},
+    {"dec.pfk", 0},          {"dec.auto", 1},    {"dec.gnorm", 0},   {"dec.pfdn", 0},
+    {"dec.fnorm", 0},        {"dec.fswi", 0},    {"pf.fswi", 2},     {"dec.fdn", 0},
+    {"dec.frope", 0},        {"dec.rec", 1},     {"dec.cols", 16},   {"dec.slices", 16},
+    {"dn.sscale", 0},        {"dn.oscale", 0},   {"dn.tscale", 0},
+};
+
+struct Tune {
+    std::map<std::string, uint32_t> v;
+    std::vector<uint32_t> mv_persists;
+    std::vector<std::string> given;
+    bool block_set = false, gemm_set = false, moe_tile_set = false, sdpa_set = false;
+
+    Tune() {
+        for (const auto& k : kKeys) v[k.name] = k.def;
+    }
+    uint32_t operator[](const char* k) const { return v.at(k); }
+
+    // Rust's u32::from_str errors, as `--tune {kv}: {e}` prints them.
+    static bool parse_u32(const std::string& s, uint32_t* out, std::string* err) {
+        if (s.empty()) {
+            *err = "cannot parse integer from empty string";
+            return false;
+        }
+        uint64_t n = 0;
+        size_t i = s[0] == '+' ? 1 : 0;
+        if (i == s.size()) {
+            *err = "invalid digit found in string";
+            return false;
+        }
+        for (; i < s.size(); i++) {
+            if (s[i] < '0' || s[i] > '9') {
+                *err = "invalid digit found in string";
+                return false;
+            }
+            n = n * 10 + (uint64_t)(s[i] - '0');
+            if (n > 0xffffffffull) {
+                *err = "number too large to fit in target type";
+                return false;
+            }
+        }
+        *out = (uint32_t)n;
+        return true;
+    }
+
+    // Tune::apply (qwen.rs:296-389): "key=value" settings, comma separated.
+    bool apply(const std::string& list, std::string* err) {
+        std::stringstream ss(list);
+        std::string kv;
+        while (std::getline(ss, kv, ',')) {
+            if (kv.empty()) continue;
+            size_t eq = kv.find('=');
+            if (eq == std::string::npos) {
+                *err = "--tune " + kv + ": key=value";
+                return false;
+            }
+            std::string key = kv.substr(0, eq), value = kv.substr(eq + 1);
+            given.push_back(key);
+            if (key == "mv.persists") {
+                mv_persists.clear();
+                std::stringstream vs(value);
+                std::string item;
+                while (std::getline(vs, item, '/')) {
+                    if (item.empty()) continue;
+                    uint32_t n;
+                    std::string e;
+                    if (!parse_u32(item, &n, &e)) {
+                        *err = "--tune " + kv + ": " + e;
+                        return false;
+                    }
+                    mv_persists.push_back(n);
+                }
+                continue;
+            }
+            uint32_t n;
+            std::string e;
+            if (!parse_u32(value, &n, &e)) {
+                *err = "--tune " + kv + ": " + e;
+                return false;
+            }
+            if (!v.count(key)) {
+                *err = "--tune " + key + ": unknown";
+                return false;
+            }
+            if (key == "prefill.block") {
+                v[key] = std::max<uint32_t>(n, 1);
+                block_set = true;
+            } else if (key == "sdpa.prefill") {
+                v[key] = n;
+                sdpa_set = true;
+            } else if (key == "gemm.mma" || key == "gemm.tn" || key == "gemm.mform" ||
+                       key == "q4.fuse") {
+                v[key] = n;
+                gemm_set = true;
+            } else if (key == "moe.tile") {
+                v[key] = n;
+                moe_tile_set = true;
+            } else if (key == "mv.masks" || key == "mv.split" || key == "mv.persist") {
+                v[key] = n;
+                v["mv.auto"] = 0;
+            } else if (key == "dec.sdpa") {
+                v[key] = std::min<uint32_t>(n, 64);
+            } else {
+                v[key] = n;
+            }
+        }
+        return validate(err);
+    }
+
+    uint32_t mq() const {
+        if ((*this)["sdpa.mq"]) return (*this)["sdpa.mq"];
+        return (*this)["sdpa.prefill"] >= 4 ? 64 : 16;
+    }
+
+    std::string brief() const {
+        char b[160];
+        snprintf(b, sizeof b, "rec.chunk=%u sdpa.prefill=%u gemm.simt=%u", (*this)["rec.chunk"],
+                 (*this)["sdpa.prefill"], (*this)["gemm.simt"]);
+        return b;
+    }
+
+    // The checks of Tune::apply (qwen.rs:367-388) that concern settings this
+    // library reads or that the reference refuses outright.
+    bool validate(std::string* err) const {
+        char b[256];
+        const Tune& t = *this;
+        if (t["q4.fuse"] > 1 || (t["q4.fuse"] == 1 && t["gemm.mma"] != 1)) {
+            snprintf(b, sizeof b, "--tune q4.fuse=%u: 0, or 1 with gemm.mma=1", t["q4.fuse"]);
+            *err = b;
+            return false;
+        }
+        uint32_t mma = t["gemm.mma"], tn = t["gemm.tn"];
+        bool tn_ok = tn == 16 || tn == 32 || tn == 64 || (mma == 3 && tn == 128);
+        if (mma > 3 || !tn_ok || t["gemm.mform"] > 9) {
+            snprintf(b, sizeof b,
+                     "--tune gemm.mma=%u gemm.tn=%u gemm.mform=%u: gemm.mma 0..2, gemm.tn 16, 32 "
+                     "or 64, gemm.mform 0..9",
+                     mma, tn, t["gemm.mform"]);
+            *err = b;
+            return false;
+        }
+        uint32_t mt = t["moe.tile"];
+        if (mt != 16 && mt != 32 && mt != 64) {
+            snprintf(b, sizeof b, "--tune moe.tile=%u: 16, 32 or 64", mt);
+            *err = b;
+            return false;
+        }
+        if (t["rec.chunk"] > 4 || t["sdpa.prefill"] > 7 || t["gemm.simt"] < 1 || t["gemm.simt"] > 2) {
+            *err = "--tune: rec.chunk 0..4, sdpa.prefill 0..7, gemm.simt 1..2 (" + brief() + ")";
+            return false;
+        }
+        uint32_t mk = t["sdpa.mk"];
+        if (t["sdpa.prefill"] >= 2 && (t["sdpa.mq"] % 8 != 0 || !(mk == 8 || mk == 16 || mk == 32 || mk == 64) ||
+                                       t["prefill.block"] % mq() != 0)) {
+            *err = "--tune sdpa.prefill=2|3|4: sdpa.mq a multiple of 8 dividing prefill.block, "
+                   "sdpa.mk 8, 16, 32 or 64 (" + brief() + ")";
+            return false;
+        }
+        return true;
+    }
+
+    // Tune::summary (qwen.rs:391-398), same keys and order.
+    std::string summary() const {
+        std::string s;
+        for (const auto& k : kKeys) {
+            std::string name = k.name;
+            uint32_t val = v.at(name);
+            if (name == "sdpa.auto") val = (val && !sdpa_set) ? 1 : 0;
+            if (name == "gemm.auto") val = (val && !gemm_set) ? 1 : 0;
+            if (!s.empty()) s += " ";
+            if (name == "mv.persists") {
+                s += "mv.persists=[";
+                for (size_t i = 0; i < mv_persists.size(); i++)
+                    s += (i ? ", " : "") + std::to_string(mv_persists[i]);
+                s += "]";
+            } else {
+                s += name + "=" + std::to_string(val);
+            }
+        }
+        return s;
+    }
+};
+
+// The dense GEMM candidates of this library, in candidate order: the first
+// is the production kernel every other is checked against.  gemm.mform
+// indexes this table (gemm.mma=1).
+struct Form {
+    const char* name;
+    uint32_t bm, bn, bk, wm, wn, mfma, dbuf, dma, order;
+};
+const Form kForms[10] = {
+    {"mma", 128, 128, 64, 2, 2, 16, 1, 1, 1},
+    {"mma_x32", 128, 128, 64, 2, 2, 32, 1, 1, 1},
+    {"mma_t256", 256, 256, 64, 2, 2, 32, 1, 1, 1},
+    {"mma_t256_w8", 256, 256, 32, 4, 2, 32, 3, 1, 1},
+    {"mma_t128x256", 128, 256, 32, 2, 2, 32, 3, 1, 1},
+    {"mma_t256x128", 256, 128, 32, 2, 2, 32, 3, 1, 1},
+    {"mma_s4", 128, 128, 64, 2, 2, 16, 3, 1, 1},
+    {"mma_k32_s4", 128, 128, 32, 2, 2, 16, 3, 1, 1},
+    {"mma_reg", 128, 128, 64, 2, 2, 16, 1, 0, 0},
+    {"mma_t64", 64, 64, 32, 1, 4, 16, 0, 0, 0},
+};
+
+hb_desc form_desc(const Form& f, uint32_t k, uint32_t n, uint32_t out, bool mf) {
+    hb_desc d{};
+    d.kind = HB_KIND_GEMM;
+    d.k = k;
+    d.n = n;
+    d.out = out;
+    d.rows_of = HB_ROWS_DENSE;
+    d.m_first = mf;
+    d.bm = f.bm;
+    d.bn = f.bn;
+    d.bk = f.bk;
+    d.wm = f.wm;
+    d.wn = f.wn;
+    d.mfma = f.mfma;
+    d.dbuf = f.dbuf;
+    d.lds_dma = f.dma;
+    d.order = f.order;
+    return d;
 }
+
+hb_desc mm2d_desc(uint32_t k, uint32_t n, uint32_t out, bool mf, uint32_t tm, uint32_t tn) {
+    hb_desc d{};
+    d.kind = HB_KIND_GEMM_DIRECT;
+    d.k = k;
+    d.n = n;
+    d.out = out;
+    d.m_first = mf;
+    d.bm = tm;
+    d.bn = tn;
+    return d;
+}
+
+const char* out_name(uint32_t out) {
+    return out == HB_OUT_F32 ? "F32" : out == HB_OUT_RESIDUAL ? "Residual" : "Bf16";
+}
+
+struct Cand {
+    std::string name;
+    int32_t kernel;
+    std::vector<hb_op> ops;
+};
+
+hb_op make_op(int32_t kernel, uint32_t m, std::initializer_list<hb_range> b) {
+    hb_op op{};
+    op.kernel = kernel;
+    op.m = m;
+    op.nbind = 0;
+    for (const auto& r : b) op.bind[op.nbind++] = r;
+    return op;
+}
+
+}  // namespace
+
+struct hb_engine {
+    hb_gpu* g = nullptr;
+    Tune t;
+    std::string tune_summary, log;
+    std::map<std::string, int32_t> gemm_pick;
+    std::map<std::string, hb_desc> mv_pick;
+    std::vector<std::pair<std::string, hb_desc>> extra;  // hb_engine_add_gemm_candidate
+    double autotune_seconds = 0.0;
+    bool timed = false;
+    std::chrono::steady_clock::time_point last_timed;
+
+    void logf(const char* fmt, ...) {
+        char buf[8192];
+        va_list ap;
+        va_start(ap, fmt);
+        vsnprintf(buf, sizeof buf, fmt, ap);
+        va_end(ap);
+        fprintf(stderr, "%s\n", buf);
+        log += buf;
+        log += "\n";
+    }
+
+    // time_ops (qwen.rs:2593).
+    int time_ops(const std::vector<hb_op>& ops, uint32_t reps, double* s) {
+        return hb_time(g, ops.data(), (uint32_t)ops.size(), reps, s);
+    }
+
+    // heat (qwen.rs:2577-2591): auto.heat ms of load after > 200 ms idle.
+    int heat(const std::vector<hb_op>& ops) {
+        double heat_s = t["auto.heat"] * 1e-3;
+        if (heat_s <= 0 ||
+            (timed && std::chrono::duration<double>(std::chrono::steady_clock::now() - last_timed).count() < 0.2))
+            return HB_OK;
+        double one;
+        int rc = time_ops(ops, 1, &one);
+        if (rc) return rc;
+        uint32_t reps = (uint32_t)std::min(256.0, std::max(1.0, std::ceil(0.05 / std::max(one, 1e-6))));
+        double total = 0;
+        while (total < heat_s) {
+            double s;
+            if ((rc = time_ops(ops, reps, &s))) return rc;
+            total += s;
+        }
+        timed = true;
+        last_timed = std::chrono::steady_clock::now();
+        return HB_OK;
+    }
+
+    // pick_flagged (qwen.rs:2547-2575): reps so one run lasts ~2 ms, five
+    // interleaved rounds, medians, the fastest eligible kept; logged with
+    // `*` after the ineligible.
+    int pick_flagged(const std::string& what, const std::vector<Cand>& c,
+                     const std::vector<bool>& eligible, size_t* best, double* best_s) {
+        auto t0 = std::chrono::steady_clock::now();
+        if (c.empty() || std::none_of(eligible.begin(), eligible.end(), [](bool e) { return e; }))
+            return fail(HB_ERR_INVALID, what + ": no eligible candidate");
+        int rc = heat(c[0].ops);
+        double one;
+        if (rc || (rc = time_ops(c[0].ops, 1, &one)) || (rc = time_ops(c[0].ops, 1, &one))) return rc;
+        uint32_t reps = (uint32_t)std::min(64.0, std::max(1.0, std::ceil(2e-3 / std::max(one, 1e-6))));
+        std::vector<std::vector<double>> times(c.size());
+        for (int round = 0; round < 5; round++)
+            for (size_t i = 0; i < c.size(); i++) {
+                double s;
+                if ((rc = time_ops(c[i].ops, reps, &s))) return rc;
+                times[i].push_back(s / reps);
+            }
+        std::vector<double> med(c.size());
+        for (size_t i = 0; i < c.size(); i++) {
+            std::sort(times[i].begin(), times[i].end());
+            med[i] = times[i][times[i].size() / 2];
+        }
+        size_t b = c.size();
+        for (size_t i = 0; i < c.size(); i++)
+            if (eligible[i] && (b == c.size() || med[i] < med[b])) b = i;
+        std::string line;
+        for (size_t i = 0; i < c.size(); i++) {
+            char buf[256];
+            snprintf(buf, sizeof buf, "%s%s%s %.3f ms", i ? ", " : "", c[i].name.c_str(),
+                     eligible[i] ? "" : "*", med[i] * 1e3);
+            line += buf;
+        }
+        logf("[autotune] %s: %s -> %s", what.c_str(), line.c_str(), c[b].name.c_str());
+        autotune_seconds += std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+        timed = true;
+        last_timed = std::chrono::steady_clock::now();
+        *best = b;
+        if (best_s) *best_s = med[b];
+        return HB_OK;
+    }
+
+    // check_candidates (qwen.rs:2497-2545): each candidate on the full block
+    // and on m - m/3 - 3 rows from a zeroed output, against candidate 0; an
+    // error beyond max|ref|/64 marks it wrong, logged, never picked.  The
+    // output and state[3] are restored.
+    int check_candidates(const std::string& what, std::vector<Cand>& c,
+                         std::vector<bool>& eligible, hb_range state, hb_range out,
+                         bool f32_out, uint32_t m, uint32_t row_bytes) {
+        char* optr;
+        uint64_t osize;
+        int rc = resolve(g, out, &optr, &osize);
+        if (rc) return rc;
+        std::vector<char> before(osize);
+        if ((rc = hb_download(g, out.buf, out.offset, before.data(), osize))) return rc;
+        std::vector<std::string> wrong;
+        for (uint32_t rows : {m, std::max<uint32_t>(m - m / 3 - 3, 1)}) {
+            if (rows > m) rows = 1;
+            uint32_t st[4] = {0, 0, 0, rows};
+            if ((rc = hb_upload(g, state.buf, state.offset, st, 16))) return rc;
+            uint64_t used = std::min<uint64_t>((uint64_t)rows * row_bytes, osize);
+            auto values = [&](std::vector<float>* v) -> int {
+                std::vector<char> raw(used);
+                int r2 = hb_download(g, out.buf, out.offset, raw.data(), used);
+                if (r2) return r2;
+                if (f32_out) {
+                    v->resize(used / 4);
+                    memcpy(v->data(), raw.data(), used / 4 * 4);
+                } else {
+                    v->resize(used / 2);
+                    for (size_t i = 0; i < v->size(); i++) {
+                        uint32_t b = (uint32_t)((uint16_t*)raw.data())[i] << 16;
+                        memcpy(&(*v)[i], &b, 4);
+                    }
+                }
+                return HB_OK;
+            };
+            auto run = [&](size_t i) -> int {
+                int r2 = hb_zero(g, out.buf, out.offset, osize);
+                if (r2) return r2;
+                std::vector<hb_op> ops = c[i].ops;
+                for (auto& op : ops) op.m = rows;
+                double s;
+                return time_ops(ops, 1, &s);
+            };
+            std::vector<float> ref, got;
+            if ((rc = run(0)) || (rc = values(&ref))) return rc;
+            float scale = 1e-6f;
+            for (float x : ref) scale = std::max(scale, std::fabs(x));
+            for (size_t i = 1; i < c.size(); i++) {
+                if (!eligible[i]) continue;
+                if ((rc = run(i)) || (rc = values(&got))) return rc;
+                float err = 0;
+                for (size_t j = 0; j < ref.size(); j++) {
+                    float e = std::fabs(ref[j] - got[j]);
+                    if (!(e <= err)) err = e;  // NaN propagates as "wrong"
+                }
+                if (!(err <= scale / 64)) {
+                    eligible[i] = false;
+                    char buf[256];
+                    snprintf(buf, sizeof buf, "%s (%u rows: max err %.3e of %.3e)", c[i].name.c_str(),
+                             rows, err, scale);
+                    wrong.push_back(buf);
+                }
+            }
+        }
+        if ((rc = hb_upload(g, out.buf, out.offset, before.data(), osize))) return rc;
+        uint32_t st[4] = {0, 0, 0, m};
+        if ((rc = hb_upload(g, state.buf, state.offset, st, 16))) return rc;
+        if (!wrong.empty()) {
+            std::string l;
+            for (size_t i = 0; i < wrong.size(); i++) l += (i ? ", " : "") + wrong[i];
+            logf("[autotune] %s: wrong against %s, never picked: %s", what.c_str(), c[0].name.c_str(),
+                 l.c_str());
+        }
+        return HB_OK;
+    }
+
+    int build(const hb_desc& d, int32_t* k) { return hb_kernel_build(g, &d, k); }
+};
+
+extern "C" {
+
+int hb_engine_open(hb_gpu* g, const char* tune, hb_engine** out) {
+    *out = nullptr;
+    if (!g) return fail(HB_ERR_INVALID, "hb_engine_open: no context");
+    hb_engine* e = new hb_engine();
+    e->g = g;
+    std::string err;
+    if (tune && !e->t.apply(tune, &err)) {
+        delete e;
+        return fail(HB_ERR_INVALID, err);
+    }
+    e->tune_summary = e->t.summary();
+    *out = e;
+    return HB_OK;
+}
+
+void hb_engine_close(hb_engine* e) { delete e; }
+
+const char* hb_engine_tune_summary(hb_engine* e) { return e->tune_summary.c_str(); }
+
+const char* hb_engine_log(hb_engine* e) { return e->log.c_str(); }
+
+double hb_engine_autotune_seconds(hb_engine* e) { return e->autotune_seconds; }
+
+int hb_tune_check(const char* tune, char* summary, uint64_t cap) {
+    Tune t;
+    std::string err;
+    if (tune && !t.apply(tune, &err)) return fail(HB_ERR_INVALID, err);
+    std::string s = t.summary();
+    if (summary && cap) {
+        size_t n = std::min<size_t>(s.size(), cap - 1);
+        memcpy(summary, s.data(), n);
+        summary[n] = 0;
+    }
+    return HB_OK;
+}
+
+int hb_engine_buckets(hb_engine* e, uint32_t* out, uint32_t cap, uint32_t* count) {
+    // qwen.rs:1051-1063: m in {64, 128, 256, ...} below prefill.block, then it.
+    std::vector<uint32_t> b;
+    uint32_t block = e->t["prefill.block"];
+    for (uint32_t m = 64; m < block; m *= 2) b.push_back(m);
+    b.push_back(block);
+    *count = (uint32_t)b.size();
+    for (uint32_t i = 0; i < b.size() && i < cap; i++) out[i] = b[i];
+    return HB_OK;
+}
+
+int hb_engine_add_gemm_candidate(hb_engine* e, const char* name, const hb_desc* desc) {
+    e->extra.emplace_back(name ? name : "extra", *desc);
+    return HB_OK;
+}
+
+int hb_engine_log_summary(hb_engine* e) {
+    e->logf("[hip] %zu kernels compiled in %.1f s, GEMMs and blocks timed in %.1f s",
+            e->g->kernels.size(), e->g->compile_seconds, e->autotune_seconds);
+    return HB_OK;
+}
+
+int hb_engine_gemm(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, hb_range state,
+                   hb_range w, hb_range x, hb_range y, uint32_t m, int32_t* kernel) {
+    const Tune& t = e->t;
+    bool mf = t["gemm.mfirst"] != 0;
+    int rc;
+    if (!t["gemm.auto"] || t.gemm_set) {
+        // The kernel gemm.mma / gemm.tn / gemm.mform name, nothing timed.
+        hb_desc d{};
+        switch (t["gemm.mma"]) {
+            case 0:
+                d.kind = HB_KIND_GEMM_SIMT;
+                d.k = k;
+                d.n = n;
+                d.out = out;
+                d.m_first = mf;
+                break;
+            case 2: d = mm2d_desc(k, n, out, mf, 64, t["gemm.tn"]); break;
+            case 3: d = form_desc(kForms[3], k, n, out, mf); break;
+            default: d = form_desc(kForms[t["gemm.mform"]], k, n, out, mf); break;
+        }
+        return e->build(d, kernel);
+    }
+    char key[128];
+    snprintf(key, sizeof key, "%ux%u %s, %u rows", k, n, out_name(out), m);
+    auto it = e->gemm_pick.find(key);
+    if (it != e->gemm_pick.end()) {
+        *kernel = it->second;
+        return HB_OK;
+    }
+    std::string what = std::string("gemm ") + key;
+    std::vector<Cand> c;
+    std::vector<bool> eligible;
+    auto add = [&](const std::string& name, const hb_desc& d) {
+        int32_t kk;
+        int r = e->build(d, &kk);
+        if (r) {
+            e->logf("[autotune] gemm %s: %s not built (%s)", key, name.c_str(), hb_last_error());
+            return;
+        }
+        c.push_back({name, kk, {make_op(kk, m, {state, w, x, y, state, state})}});
+        eligible.push_back(true);
+    };
+    for (const auto& f : kForms) add(f.name, form_desc(f, k, n, out, mf));
+    if (c.empty() || c[0].name != "mma")
+        return fail(HB_ERR_COMPILE, what + ": the production kernel mma is not built: " + hb_last_error());
+    for (auto tm_tn : {std::make_pair(64u, 64u), std::make_pair(64u, 32u), std::make_pair(32u, 64u),
+                       std::make_pair(32u, 32u), std::make_pair(64u, 16u), std::make_pair(32u, 16u)}) {
+        char nm[32];
+        snprintf(nm, sizeof nm, "mm2d%ux%u", tm_tn.first, tm_tn.second);
+        add(nm, mm2d_desc(k, n, out, mf, tm_tn.first, tm_tn.second));
+    }
+    for (const auto& ex : e->extra) {
+        hb_desc d = ex.second;
+        add(ex.first, d);
+    }
+    uint32_t row_bytes = n * (out == HB_OUT_F32 ? 4 : 2);
+    if ((rc = e->check_candidates(what, c, eligible, state, y, out == HB_OUT_F32, m, row_bytes))) return rc;
+    size_t best;
+    if ((rc = e->pick_flagged(what, c, eligible, &best, nullptr))) return rc;
+    e->gemm_pick[key] = c[best].kernel;
+    *kernel = c[best].kernel;
+    return HB_OK;
+}
+
+int hb_engine_matvec(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, uint32_t mv_m,
+                     const hb_range* ws, uint32_t nws, hb_range x, hb_range y, int32_t* kernel) {
+    const Tune& t = e->t;
+    if (!nws) return fail(HB_ERR_INVALID, "matvec: no weights");
+    auto desc = [&](uint32_t form, uint32_t rows, uint32_t split, uint32_t persist) {
+        hb_desc d{};
+        d.kind = HB_KIND_MATVEC;
+        d.k = k;
+        d.n = n;
+        d.out = out;
+        d.mv_m = mv_m;
+        d.form = form;
+        d.rows = rows;
+        d.split = split;
+        d.persist = persist;
+        d.unroll = 4;
+        return d;
+    };
+    if (!t["mv.auto"]) {
+        // mv.split / mv.persist, the engine's rows (Options::matvec_rows).
+        uint32_t rows = std::max<uint32_t>(1, std::min<uint32_t>(4, 64 / std::max<uint32_t>(mv_m, 1)));
+        return e->build(desc(0, rows, t["mv.split"], t["mv.persist"]), kernel);
+    }
+    std::string persists;
+    if (!t.mv_persists.empty()) {
+        persists = " p[";
+        for (size_t i = 0; i < t.mv_persists.size(); i++)
+            persists += (i ? ", " : "") + std::to_string(t.mv_persists[i]);
+        persists += "]";
+    }
+    char key[160];
+    snprintf(key, sizeof key, "%ux%u %s m%u%s", k, n, out_name(out), mv_m, persists.c_str());
+    auto it = e->mv_pick.find(key);
+    if (it != e->mv_pick.end()) return e->build(it->second, kernel);
+    // Each form timed over every matrix of the shape (mv.cold) or the first.
+    uint32_t nw = t["mv.cold"] ? nws : 1;
+    std::vector<Cand> c;
+    std::vector<hb_desc> descs;
+    std::vector<uint32_t> splits = t["mv.splitauto"] ? std::vector<uint32_t>{1, 2, 4} : std::vector<uint32_t>{1};
+    std::vector<uint32_t> pers = {0};
+    for (uint32_t p : t.mv_persists) pers.push_back(p);
+    auto add = [&](const std::string& name, const hb_desc& d) {
+        int32_t kk;
+        if (e->build(d, &kk)) {
+            e->logf("[autotune] matvec %s: %s not built (%s)", key, name.c_str(), hb_last_error());
+            return;
+        }
+        std::vector<hb_op> ops;
+        for (uint32_t i = 0; i < nw; i++) ops.push_back(make_op(kk, mv_m, {ws[i], x, y}));
+        c.push_back({name, kk, ops});
+        descs.push_back(d);
+    };
+    for (uint32_t split : splits)
+        for (uint32_t p : pers)
+            for (uint32_t rows : {1u, 2u, 4u, 8u}) {
+                if (rows * mv_m > 64 || (p > 0 && rows == 8)) continue;
+                std::string tag = (split > 1 ? "k" + std::to_string(split) : "") +
+                                  (p ? "p" + std::to_string(p) : "");
+                add("r" + std::to_string(rows) + tag, desc(0, rows, split, p));
+            }
+    for (uint32_t split : splits)
+        for (uint32_t p : pers) {
+            std::string tag = (split > 1 ? "k" + std::to_string(split) : "") + (p ? "p" + std::to_string(p) : "");
+            add("mfma" + tag, desc(1, 16, split, p));
+        }
+    if (c.empty()) return fail(HB_ERR_COMPILE, std::string("matvec ") + key + ": no form built");
+    std::vector<bool> all(c.size(), true);
+    size_t best;
+    int rc = e->pick_flagged(std::string("matvec ") + key, c, all, &best, nullptr);
+    if (rc) return rc;
+    e->mv_pick[key] = descs[best];
+    *kernel = c[best].kernel;
+    return HB_OK;
+}
+
+int hb_engine_experts(hb_engine* e, uint32_t experts, uint32_t top_k, uint32_t hidden,
+                      uint32_t inter, uint32_t m, const hb_moe_io* io, int32_t kernels[4],
+                      uint32_t* bm_out) {
+    const Tune& t = e->t;
+    bool mf = t["gemm.mfirst"] != 0;
+    int rc;
+    auto sort_desc = [&](bool atomic, uint32_t bm) {
+        hb_desc d{};
+        d.kind = atomic ? HB_KIND_SORT_ATOMIC : HB_KIND_SORT;
+        d.experts = experts;
+        d.top_k = top_k;
+        d.bm = bm;
+        d.rows_max = m;
+        return d;
+    };
+    // An expert GEMM over tiles of bm rows: W rows by bn, four waves along N.
+    auto gemm_desc = [&](uint32_t k, uint32_t n, uint32_t rows_of, uint32_t bm, uint32_t bn) {
+        hb_desc d{};
+        d.kind = HB_KIND_GEMM;
+        d.k = k;
+        d.n = n;
+        d.out = HB_OUT_BF16;
+        d.rows_of = rows_of;
+        d.m_first = mf;
+        d.bm = bm;
+        d.bn = bn;
+        d.bk = 64;
+        d.wm = 1;
+        d.wn = 4;
+        d.mfma = 16;
+        d.lds_dma = (bm * 8) % 256 == 0 && (k / 64) % 2 == 0 ? 1 : 0;
+        d.dbuf = 1;
+        d.top_k = top_k;
+        d.experts = experts;
+        d.tiles = (m * top_k + bm - 1) / bm + experts;  // moe_tiles
+        d.rows_max = m;
+        return d;
+    };
+    hb_desc gd{};
+    gd.kind = HB_KIND_GATHER;
+    gd.n = hidden;
+    gd.top_k = top_k;
+    int32_t gather;
+    if ((rc = e->build(gd, &gather))) return rc;
+    auto kernels_for = [&](uint32_t bm, int32_t* sort, int32_t* gu, int32_t* dn) -> int {
+        int r;
+        if ((r = e->build(sort_desc(false, bm), sort))) return r;
+        if ((r = e->build(gemm_desc(hidden, 2 * inter, HB_ROWS_GATHER, bm, 128), gu))) return r;
+        return e->build(gemm_desc(inter, hidden, HB_ROWS_SCATTER, bm, 128), dn);
+    };
+    if (!t["gemm.auto"] || t.gemm_set) {
+        uint32_t bm = t["moe.tile"];
+        if ((rc = kernels_for(bm, &kernels[0], &kernels[1], &kernels[2]))) return rc;
+        kernels[3] = -1;
+        *bm_out = bm;
+        return HB_OK;
+    }
+    auto gu_ops = [&](int32_t k, hb_range xin) {
+        return make_op(k, m, {io->state, io->w_gate_up, xin, io->egu, io->list, io->tiles});
+    };
+    hb_op dn_op = make_op(0, m, {io->state, io->w_down, io->ehb, io->ey, io->list, io->tiles});
+    hb_op g_op = make_op(gather, m, {io->state, io->list, io->x, io->xs});
+    std::vector<uint32_t> tiles_rows = t.moe_tile_set ? std::vector<uint32_t>{t["moe.tile"]}
+                                                      : std::vector<uint32_t>{16, 32, 64};
+    double best_total = 1e30;
+    for (uint32_t bm : tiles_rows) {
+        int32_t scan, atomic, mma_gu, mma_dn;
+        if ((rc = kernels_for(bm, &scan, &mma_gu, &mma_dn))) return rc;
+        if ((rc = e->build(sort_desc(true, bm), &atomic))) return rc;
+        auto sort_op = [&](int32_t k) {
+            return std::vector<hb_op>{make_op(k, m, {io->state, io->route, io->list, io->tiles})};
+        };
+        char what[160];
+        snprintf(what, sizeof what, "experts sort by %u rows, %u rows", bm, m);
+        std::vector<Cand> cs = {{"scan", scan, sort_op(scan)}, {"atomic", atomic, sort_op(atomic)}};
+        size_t bs;
+        double s_sort;
+        if ((rc = e->pick_flagged(what, cs, {true, true}, &bs, &s_sort))) return rc;
+        // The list and table of these tiles, by the sort kept.
+        double tmp;
+        if ((rc = e->time_ops(cs[bs].ops, 1, &tmp))) return rc;
+        std::vector<Cand> cgu, cdn;
+        auto add_gu = [&](const std::string& name, const hb_desc& d, bool gathered) {
+            int32_t k;
+            if (e->build(d, &k)) {
+                e->logf("[autotune] experts: %s by %u rows not built (%s)", name.c_str(), bm, hb_last_error());
+                return;
+            }
+            std::vector<hb_op> ops;
+            if (gathered) ops.push_back(g_op);
+            ops.push_back(gu_ops(k, gathered ? io->xs : io->x));
+            cgu.push_back({name, k, ops});
+        };
+        auto add_dn = [&](const std::string& name, const hb_desc& d) {
+            int32_t k;
+            if (e->build(d, &k)) {
+                e->logf("[autotune] experts: %s by %u rows not built (%s)", name.c_str(), bm, hb_last_error());
+                return;
+            }
+            hb_op op = dn_op;
+            op.kernel = k;
+            cdn.push_back({name, k, {op}});
+        };
+        add_gu("mma", gemm_desc(hidden, 2 * inter, HB_ROWS_GATHER, bm, 128), false);
+        add_gu("mma_n256", gemm_desc(hidden, 2 * inter, HB_ROWS_GATHER, bm, 256), false);
+        add_gu("gather+mma", gemm_desc(hidden, 2 * inter, HB_ROWS_SORTED, bm, 128), true);
+        add_dn("mma", gemm_desc(inter, hidden, HB_ROWS_SCATTER, bm, 128));
+        add_dn("mma_n256", gemm_desc(inter, hidden, HB_ROWS_SCATTER, bm, 256));
+        size_t bgu, bdn;
+        double s_gu, s_dn;
+        snprintf(what, sizeof what, "experts gate_up %ux%u by %u rows, %u rows", hidden, 2 * inter, bm, m);
+        if ((rc = e->pick_flagged(what, cgu, std::vector<bool>(cgu.size(), true), &bgu, &s_gu))) return rc;
+        snprintf(what, sizeof what, "experts down %ux%u by %u rows, %u rows", inter, hidden, bm, m);
+        if ((rc = e->pick_flagged(what, cdn, std::vector<bool>(cdn.size(), true), &bdn, &s_dn))) return rc;
+        double total = s_gu + s_dn + s_sort;
+        e->logf("[autotune] experts by %u rows, %u rows: sort %.3f ms, total %.3f ms", bm, m,
+                s_sort * 1e3, total * 1e3);
+        if (total < best_total) {
+            best_total = total;
+            kernels[0] = cs[bs].kernel;
+            kernels[1] = cgu[bgu].kernel;
+            kernels[2] = cdn[bdn].kernel;
+            kernels[3] = cgu[bgu].ops.size() > 1 ? gather : -1;
+            *bm_out = bm;
+        }
+    }
+    e->logf("[autotune] experts, %u rows -> tiles of %u rows", m, *bm_out);
+    return HB_OK;
+}
+
+}  // extern "C"

@@ -32,7 +32,8 @@
 //    contiguous range of tiles (its own L2 keeps their panels).
 //
 // Compile-time constants (-D): HB_K, HB_N, HB_OUT (0 bf16, 1 f32, 2
-// residual), HB_ROWS (0 dense, 1 gather, 2 scatter), HB_TOPK, HB_BM, HB_BN,
+// residual), HB_ROWS (0 dense, 1 gather, 2 scatter, 3 sorted: row p of X
+// and of Y, the rows a gather put in sorted order), HB_TOPK, HB_BM, HB_BN,
 // HB_BK, HB_WM, HB_WN, HB_MFMA (16|32), HB_STAGES (1..4), HB_SWZ, HB_ORDER,
 // HB_MFIRST, HB_DMA.
 //
@@ -171,7 +172,7 @@ extern "C" __global__ __launch_bounds__(NT) void hb_kernel(
         if constexpr (ROWS == 1) {
             u32 pr = list[row0 + rr] / TOPK;
             return pr < m_launch ? pr : m_launch - 1;
-        } else if constexpr (ROWS == 2) {
+        } else if constexpr (ROWS == 2 || ROWS == 3) {
             u32 p = row0 + rr;
             return p < pairs ? p : pairs - 1;
         } else {

@@ -80,6 +80,7 @@ class Rows(enum.IntEnum):
     Dense = 0
     Gather = 1
     Scatter = 2
+    Sorted = 3
 
 
 class Range(ctypes.Structure):
@@ -224,6 +225,16 @@ def gemm_mma_rows(kdim, n, out, m_first=True, rows_of=Rows.Dense, top_k=0, tiles
                 top_k=top_k, tiles=tiles, bm=bm, experts=experts, rows_max=rows_max, **tile)
 
 
+def gemm_simt(kdim, n, out, m_first=True):
+    """gemm_simt (prefill.rs:133): the VALU GEMM, the contract's summation order."""
+    return Desc(kind=Kind.GEMM_SIMT, k=kdim, n=n, out=out, m_first=m_first)
+
+
+def gemm_mm2d(kdim, n, out, tm=64, tn=64, m_first=True):
+    """gemm_mm2d (prefill.rs:442): MFMA operands straight from memory, tm x tn tiles."""
+    return Desc(kind=Kind.GEMM_DIRECT, k=kdim, n=n, out=out, bm=tm, bn=tn, m_first=m_first)
+
+
 def gemm_mma(kdim, n, out, m_first=True, **tile):
     """gemm_mma (prefill.rs:418): the dense MFMA GEMM."""
     return gemm_mma_rows(kdim, n, out, m_first, Rows.Dense, **tile)
@@ -332,3 +343,141 @@ class Gpu:
 def r(buf, offset=0, size=0):
     """Range over a buffer (`Range::whole` when offset and size are 0)."""
     return Range(int(buf), 0, int(offset), int(size))
+
+
+lib.hb_engine_log.argtypes = [_P]
+lib.hb_engine_log.restype = ctypes.c_char_p
+lib.hb_engine_log_summary.argtypes = [_P]
+lib.hb_engine_add_gemm_candidate.argtypes = [_P, ctypes.c_char_p, ctypes.POINTER(Desc)]
+lib.hb_tune_check.argtypes = [ctypes.c_char_p, ctypes.c_char_p, _u64]
+
+
+def tune_check(tune):
+    """Tune::apply + Tune::summary (qwen.rs:296-398) without a device: the
+    summary, or HerbertError with the reference's message."""
+    buf = ctypes.create_string_buffer(8192)
+    check(lib.hb_tune_check(tune.encode(), buf, len(buf)))
+    return buf.value.decode()
+
+
+class Engine:
+    """The kernel-selection part of QwenEngine (qwen.rs): --tune settings,
+    gemm (:2200), mv_full (:1311), expert_pipes (:2326), with the
+    [autotune] log."""
+
+    def __init__(self, gpu, tune=""):
+        h = _P()
+        check(lib.hb_engine_open(gpu.h, tune.encode(), ctypes.byref(h)))
+        self.h = h
+        self.gpu = gpu
+
+    def close(self):
+        if self.h:
+            lib.hb_engine_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def tune_summary(self):
+        return lib.hb_engine_tune_summary(self.h).decode()
+
+    def log(self):
+        return lib.hb_engine_log(self.h).decode()
+
+    def log_summary(self):
+        check(lib.hb_engine_log_summary(self.h))
+
+    def autotune_seconds(self):
+        return lib.hb_engine_autotune_seconds(self.h)
+
+    def buckets(self):
+        out = (_u32 * 32)()
+        n = _u32()
+        check(lib.hb_engine_buckets(self.h, out, 32, ctypes.byref(n)))
+        return list(out[:n.value])
+
+    def add_gemm_candidate(self, name, desc):
+        check(lib.hb_engine_add_gemm_candidate(self.h, name.encode(), ctypes.byref(desc)))
+
+    def gemm(self, k, n, out, state, w, x, y, m):
+        kern = _i32()
+        check(lib.hb_engine_gemm(self.h, k, n, int(out), state, w, x, y, m, ctypes.byref(kern)))
+        return kern.value
+
+    def mv(self, k, n, out, mv_m, ws, x, y):
+        arr = (Range * len(ws))(*ws)
+        kern = _i32()
+        check(lib.hb_engine_matvec(self.h, k, n, int(out), mv_m, arr, len(ws), x, y,
+                                   ctypes.byref(kern)))
+        return kern.value
+
+    def experts(self, experts, top_k, hidden, inter, m, io):
+        """io: MoeIo; returns ([sort, gate_up, down, gather or -1], rows per tile)."""
+        ks = (_i32 * 4)()
+        bm = _u32()
+        check(lib.hb_engine_experts(self.h, experts, top_k, hidden, inter, m, ctypes.byref(io), ks,
+                                    ctypes.byref(bm)))
+        return list(ks), bm.value
+
+
+class MoeLayer:
+    """The routed experts of one MoE layer over blocks of up to `rows` rows,
+    in the reference's op order (qwen.rs:2705-2735): route_qwen -> moe_sort
+    -> [moe_gather] -> grouped gate|up -> swiglu_slots -> grouped down
+    (scatter to slot rows) -> moe_combine.  Owns its device buffers; the
+    kernels come from Engine.experts (expert_pipes)."""
+
+    def __init__(self, gpu, engine, experts, top_k, hidden, inter, rows, w_gate_up, w_down):
+        self.gpu, self.e, self.k, self.h, self.mi, self.rows = gpu, experts, top_k, hidden, inter, rows
+        pairs = rows * top_k
+        g = gpu
+        self.buf = {
+            "state": g.alloc_with(np.array([0, 0, 0, rows], np.uint32)),
+            "scores": g.alloc(rows * experts * 2),
+            "route": g.alloc(rows * 2 * top_k * 4),
+            "list": g.alloc(pairs * 4),
+            "tiles": g.alloc((1 + 3 * moe_tiles(rows, top_k, experts, 16)) * 4),
+            "x": g.alloc(rows * hidden * 2),
+            "w_gate_up": w_gate_up,
+            "egu": g.alloc(pairs * 2 * inter * 2),
+            "ehb": g.alloc(pairs * inter * 2),
+            "w_down": w_down,
+            "ey": g.alloc(pairs * hidden * 2),
+            "xs": g.alloc(pairs * hidden * 2),
+            "out": g.alloc(rows * hidden * 2),
+        }
+        b = self.buf
+        self.io = MoeIo(*[r(b[f]) for f in ("state", "route", "list", "tiles", "x", "w_gate_up",
+                                             "egu", "ehb", "w_down", "ey", "xs")])
+        self.route_k = gpu.pipeline(Desc(kind=Kind.ROUTE, experts=experts, top_k=top_k))
+        self.swiglu_k = gpu.pipeline(Desc(kind=Kind.SWIGLU, n=inter))
+        self.combine_k = gpu.pipeline(Desc(kind=Kind.COMBINE, n=hidden, top_k=top_k))
+        self.kernels, self.bm = engine.experts(experts, top_k, hidden, inter, rows, self.io)
+
+    def ops(self, m=None):
+        """The layer's dispatches over m rows (m <= rows; state[3] must be m)."""
+        m = self.rows if m is None else m
+        b, k = self.buf, self.k
+        sort, gu, dn, gather = self.kernels
+        ops = [Op(self.route_k, [r(b["scores"]), r(b["route"])], m),
+               Op(sort, [r(b["state"]), r(b["route"]), r(b["list"]), r(b["tiles"])], m)]
+        xin = b["x"]
+        if gather >= 0:
+            ops.append(Op(gather, [r(b["state"]), r(b["list"]), r(b["x"]), r(b["xs"])], m))
+            xin = b["xs"]
+        ops.append(Op(gu, [r(b["state"]), r(b["w_gate_up"]), r(xin), r(b["egu"]), r(b["list"]),
+                           r(b["tiles"])], m))
+        ops.append(Op(self.swiglu_k, [r(b["egu"]), r(b["ehb"])], m * k))
+        ops.append(Op(dn, [r(b["state"]), r(b["w_down"]), r(b["ehb"]), r(b["ey"]), r(b["list"]),
+                           r(b["tiles"])], m))
+        ops.append(Op(self.combine_k, [r(b["ey"]), r(b["route"]), r(b["out"])], m))
+        return ops
+
+    def free(self):
+        for name, buf in self.buf.items():
+            if name not in ("w_gate_up", "w_down"):
+                self.gpu.free(buf)

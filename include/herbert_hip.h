@@ -87,7 +87,11 @@ enum hb_out { /* Out (kernels.rs:30-43) */
 enum hb_rows { /* MmaRows (prefill.rs:317-338) */
     HB_ROWS_DENSE = 0,
     HB_ROWS_GATHER = 1,
-    HB_ROWS_SCATTER = 2
+    HB_ROWS_SCATTER = 2,
+    /* sorted row p reads X[p] and writes Y[p] with its tile's expert: the
+     * [gate|up] GEMM after moe_gather (the gather+mm2d candidate of
+     * expert_pipes, qwen.rs:2358) */
+    HB_ROWS_SORTED = 3
 };
 
 typedef struct hb_desc {
@@ -215,6 +219,21 @@ int hb_engine_experts(hb_engine *engine, uint32_t experts, uint32_t top_k, uint3
 
 /* Seconds the engine spent timing candidates (autotune_seconds). */
 double hb_engine_autotune_seconds(hb_engine *engine);
+
+/* Every line the engine logged ([autotune] ..., [hip] ...), also written to
+ * stderr as the reference's eprintln! does. */
+const char *hb_engine_log(hb_engine *engine);
+/* The load's closing line, the reference's "[metal] N kernels compiled in
+ * ..., GEMMs and blocks timed in ..." (qwen.rs:1069), as "[hip] ...". */
+int hb_engine_log_summary(hb_engine *engine);
+/* One more candidate for the engine's next GEMM choices, after the built-in
+ * ones (the way check_candidates meets a kernel that builds but computes
+ * something else, qwen.rs:2488-2496: it must be logged wrong, never picked). */
+int hb_engine_add_gemm_candidate(hb_engine *engine, const char *name, const hb_desc *desc);
+/* Tune::default + Tune::apply + Tune::summary without a device: HB_OK and
+ * the summary in `summary` (cap bytes), or HB_ERR_INVALID and the
+ * reference's message in hb_last_error(). */
+int hb_tune_check(const char *tune, char *summary, uint64_t cap);
 
 #ifdef __cplusplus
 }

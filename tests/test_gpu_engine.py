@@ -1,0 +1,128 @@
+"""The selection layer on the GPU (qwen.rs gemm :2200, check_candidates
+:2497, pick_flagged :2547, mv_full :1311, expert_pipes :2326): candidates
+checked against the first, a wrong one logged and never picked, an
+unbuildable one skipped, the [autotune] lines in the reference's format,
+and the kernels picked computing the contract (the whole MoE layer through
+the picked kernels against the oracle)."""
+import re
+
+import numpy as np
+import pytest
+
+import herbert_hip as hb
+import hb_oracle as orc
+from parity import abs_products, check_close
+
+pytestmark = pytest.mark.gpu
+
+
+def test_gemm_autotune_checks_and_picks(gpu, capfd):
+    m, k, n = 512, 1024, 3584
+    x = hb.normal_bf16(0x5EED0001, 1.0, (m, k))
+    w = hb.normal_bf16(0x5EED0002, 0.02, (n, k))
+    st, W, X = gpu.alloc_with(np.array([0, 0, 0, m], np.uint32)), gpu.alloc_with(w), gpu.alloc_with(x)
+    Y = gpu.alloc(m * n * 2)
+    with hb.Engine(gpu, "") as e:
+        # a kernel that builds and runs but computes another function: the
+        # same GEMM with half the K (rows read at the wrong stride)
+        wrong = hb.gemm_mma(k // 2, n, 0, bm=128, bn=128, bk=64, wm=2, wn=2, mfma=16, dbuf=1,
+                            lds_dma=1, order=1)
+        e.add_gemm_candidate("halfk", wrong)
+        e.add_gemm_candidate("bk48", hb.gemm_mma(k, n, 0, bk=48))  # does not build
+        kern = e.gemm(k, n, 0, hb.r(st), hb.r(W), hb.r(X), hb.r(Y), m)
+        log = e.log()
+        again = e.gemm(k, n, 0, hb.r(st), hb.r(W), hb.r(X), hb.r(Y), m)
+        assert again == kern  # cached under the shape key
+        e.log_summary()
+        assert "[hip] " in e.log()
+    print(log)
+    assert re.search(r"\[autotune\] gemm 1024x3584 Bf16, 512 rows: bk48 not built", log)
+    assert re.search(r"\[autotune\] gemm 1024x3584 Bf16, 512 rows: wrong against mma, never "
+                     r"picked: halfk \(512 rows: max err [0-9.e+-]+ of [0-9.e+-]+\)$", log, re.M)
+    line = [l for l in log.splitlines() if "-> " in l][0]
+    assert line.startswith("[autotune] gemm 1024x3584 Bf16, 512 rows: mma ")
+    assert "halfk* " in line
+    picked = line.split("-> ")[1]
+    assert picked != "halfk" and gpu.kernel_name(kern)
+    # the pick computes the contract (Y is scratch while candidates are timed,
+    # as in the reference, qwen.rs:1414)
+    gpu.launch(kern, [hb.r(st), hb.r(W), hb.r(X), hb.r(Y), hb.r(st), hb.r(st)], m)
+    got = gpu.download(Y, np.uint16, m * n).reshape(m, n)
+    check_close(got, orc.gemm(x, w), k, abs_products(x, w), "picked " + picked)
+    for b in (st, W, X, Y):
+        gpu.free(b)
+
+
+def test_gemm_explicit_forms(gpu):
+    """gemm.mma / gemm.mform / gemm.tn name the kernel; nothing is timed."""
+    m, k, n = 256, 512, 1024
+    x = hb.normal_bf16(1, 1.0, (m, k))
+    w = hb.normal_bf16(2, 0.02, (n, k))
+    st, W, X = gpu.alloc_with(np.array([0, 0, 0, m], np.uint32)), gpu.alloc_with(w), gpu.alloc_with(x)
+    Y = gpu.alloc(m * n * 2)
+    want = orc.gemm(x, w)
+    for tune in ["gemm.mma=0", "gemm.mma=2,gemm.tn=32", "gemm.mma=3"] + \
+            ["gemm.mform=%d" % f for f in range(10)]:
+        with hb.Engine(gpu, tune) as e:
+            kern = e.gemm(k, n, 0, hb.r(st), hb.r(W), hb.r(X), hb.r(Y), m)
+            assert e.log() == ""
+        gpu.launch(kern, [hb.r(st), hb.r(W), hb.r(X), hb.r(Y), hb.r(st), hb.r(st)], m)
+        got = gpu.download(Y, np.uint16, m * n).reshape(m, n)
+        st_ = check_close(got, want, k, abs_products(x, w), tune)
+        if tune == "gemm.mma=0":
+            assert st_["exact"] == 1.0  # the VALU GEMM sums in the contract's order
+    for b in (st, W, X, Y):
+        gpu.free(b)
+
+
+def test_matvec_autotune_cold(gpu):
+    k, n, m = 2560, 4608, 4
+    ws = [hb.normal_bf16(10 + i, 0.02, (n, k)) for i in range(3)]
+    x = hb.normal_bf16(9, 1.0, (m, k))
+    Wb = [gpu.alloc_with(w) for w in ws]
+    X, Y = gpu.alloc_with(x), gpu.alloc(m * n * 2)
+    with hb.Engine(gpu, "") as e:
+        kern = e.mv(k, n, 0, m, [hb.r(b) for b in Wb], hb.r(X), hb.r(Y))
+        log = e.log()
+    assert re.search(r"\[autotune\] matvec 2560x4608 Bf16 m4: r1 .* -> ", log), log
+    gpu.launch(kern, [hb.r(Wb[1]), hb.r(X), hb.r(Y)], m)
+    got = gpu.download(Y, np.uint16, m * n).reshape(m, n)
+    check_close(got, orc.gemm(x, ws[1]), k, abs_products(x, ws[1]), "mv pick")
+    for b in Wb + [X, Y]:
+        gpu.free(b)
+
+
+def test_moe_layer_through_picked_kernels(gpu):
+    """expert_pipes picks sort, grouped GEMMs and tile rows; the whole routed
+    layer through them equals the oracle's (route, sort, gather, GEMMs,
+    SwiGLU, combine), the GEMM rounding within the contract."""
+    E, K_, H, MI, rows = 64, 8, 512, 256, 256
+    wgu = hb.normal_bf16(21, 0.02, (E * 2 * MI, H))
+    wdn = hb.normal_bf16(22, 0.02, (E * H, MI))
+    Wgu, Wdn = gpu.alloc_with(wgu), gpu.alloc_with(wdn)
+    scores = hb.normal_bf16(23, 1.0, (rows, E))
+    x = hb.normal_bf16(24, 1.0, (rows, H))
+    with hb.Engine(gpu, "") as e:
+        layer = hb.MoeLayer(gpu, e, E, K_, H, MI, rows, Wgu, Wdn)
+        log = e.log()
+    assert "[autotune] experts, 256 rows -> tiles of" in log
+    assert re.search(r"\[autotune\] experts sort by 16 rows, 256 rows: scan .*atomic", log)
+    gpu.upload(layer.buf["scores"], scores)
+    gpu.upload(layer.buf["x"], x)
+    gpu.time_ops(layer.ops(), 1)
+    out = gpu.download(layer.buf["out"], np.uint16, rows * H).reshape(rows, H)
+    route = orc.route(scores, K_)
+    assert np.array_equal(gpu.download(layer.buf["route"], np.uint32, rows * 2 * K_).reshape(rows, -1), route)
+    lst, tiles = orc.moe_sort(route, K_, E, layer.bm)
+    gu = orc.experts_gemm(x, wgu, lst, tiles, H, 2 * MI, 1, K_, rows * K_)
+    h = orc.swiglu(gu, MI)
+    ey = orc.experts_gemm(h, wdn, lst, tiles, MI, H, 2, K_, rows * K_)
+    want = orc.combine(ey, route, K_, H)
+    from parity import bf16_to_f32
+    err = np.abs(bf16_to_f32(out).astype(np.float64) - bf16_to_f32(want))
+    scale = np.abs(bf16_to_f32(want)).max()
+    assert err.max() <= scale / 64, (err.max(), scale)
+    assert np.mean(out == want) > 0.9
+    layer.free()
+    gpu.free(Wgu)
+    gpu.free(Wdn)
