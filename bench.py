@@ -1,0 +1,195 @@
+"""Benchmark of the bf16 matrix-multiplication path on one MI355X.
+
+The step (the metric's M=2048 case): the four
+prefill GEMMs of one layer of a 4B-class dense model at M=2048 rows --
+QKV 2560->4608 (Out::Bf16), O 4096->2560 (Out::Residual), gate|up
+2560->18432 (Out::Bf16), down 9216->2560 (Out::Residual) -- with bf16
+inputs ~N(0,1) / N(0,0.02) from the seeded generator, f32 accumulation and
+one rounding at the output, each GEMM on the kernel the selection layer
+picked at load (QwenEngine::gemm with gemm.auto, src/metal/qwen.rs:2200).
+`value` = the step's algorithmic flops (2*M*N*K summed) / its GPU time,
+inputs resident in HBM, timed with HIP events on the library's stream.
+
+Also reported (the metric's second half): the decode matvec, M=1, over
+four layers of the same weights plus the lm_head (K=2560, N=151936), 2.2 GB
+streamed per step, as GB/s of algorithmic bytes (2*N*K + 2*M*K + 2*M*N per
+projection, + 2*M*N for Residual) against HBM's 8 TB/s.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--tune key=value,...]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "herbert-metal-bf16_amd"))
+
+import numpy as np  # noqa: E402
+
+MFMA_BF16_PEAK = 2500.0  # TFLOP/s, dense bf16 MFMA, MI355X
+HBM_PEAK = 8000.0  # GB/s
+M = 2048
+LAYER = [("qkv", 2560, 4608, 0), ("o", 4096, 2560, 2), ("gate_up", 2560, 18432, 0),
+         ("down", 9216, 2560, 2)]
+LM_HEAD = ("lm_head", 2560, 151936, 0)
+DECODE_LAYERS = 4
+SEED = 0x5EED0002  # config 2's seeds: X = SEED + 2i, W = SEED + 2i + 1
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def cpu_baseline(rows):
+    """The contract's scalar f32 GEMM (oracle/hb_oracle.c) on the host's
+    cores over `rows` rows of each of the step's four GEMMs."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import hb_oracle as orc
+    import herbert_hip as hb
+    threads = min(16, os.cpu_count() or 1)
+    flops, secs = 0.0, 0.0
+    for i, (name, k, n, out) in enumerate(LAYER):
+        x = hb.normal_bf16(SEED + 2 * i, 1.0, (rows, k))
+        w = hb.normal_bf16(SEED + 2 * i + 1, 0.02, (n, k))
+        y0 = hb.normal_bf16(SEED + 100 + i, 1.0, (rows, n)) if out == 2 else None
+        t = time.perf_counter()
+        orc.gemm(x, w, out, y0, threads=threads)
+        secs += time.perf_counter() - t
+        flops += 2.0 * rows * n * k
+    return {"value": flops / secs / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": "%d of the %d rows of each of the 4 GEMMs (oracle/hb_oracle.c, scalar f32 "
+                      "in k order, %d threads), %.1f s" % (rows, M, threads, secs)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--tune", default="")
+    ap.add_argument("--cpu-rows", type=int, default=1536)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-matvec", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build runs on one GPU only (--gpus %d asked); the path would shard "
+              "each GEMM by N across GPUs, which is not built" % args.gpus, file=sys.stderr)
+        sys.exit(2)
+
+    import herbert_hip as hb
+    g = hb.Gpu(0)
+    log("[gpu]", g.summary())
+    e = hb.Engine(g, args.tune)
+    state = g.alloc_with(np.array([0, 0, 0, M], np.uint32))
+    bufs, ops, flops, per_gemm = [], [], 0.0, {}
+    t0 = time.time()
+    for i, (name, k, n, out) in enumerate(LAYER):
+        X = g.alloc_with(hb.normal_bf16(SEED + 2 * i, 1.0, (M, k)))
+        W = g.alloc_with(hb.normal_bf16(SEED + 2 * i + 1, 0.02, (n, k)))
+        Y = g.alloc_with(hb.normal_bf16(SEED + 100 + i, 1.0, (M, n)))
+        bufs += [X, W, Y]
+        kern = e.gemm(k, n, out, hb.r(state), hb.r(W), hb.r(X), hb.r(Y), M)
+        op = hb.Op(kern, [hb.r(state), hb.r(W), hb.r(X), hb.r(Y), hb.r(state), hb.r(state)], M)
+        ops.append(op)
+        f = 2.0 * M * n * k
+        flops += f
+        per_gemm[name] = {"kernel": g.kernel_name(kern), "flops": f, "op": op}
+    log("[bench] selection done in %.1f s" % (time.time() - t0))
+
+    # Warmup, then exactly K steps between two synchronisations.
+    g.time_ops(ops, max(args.warmup, 0)) if args.warmup > 0 else None
+    g.sync()
+    t = g.time_ops(ops, args.steps)
+    g.sync()
+    ms = t / args.steps * 1e3
+    value = flops / (t / args.steps) / 1e12
+
+    # Per-GEMM kernel time (HIP events on the library's stream), the dominant
+    # kernel's roofline.
+    for name, d in per_gemm.items():
+        reps = 20
+        d["us"] = g.time_ops([d["op"]], reps) / reps * 1e6
+        d["tflops"] = d["flops"] / (d["us"] * 1e-6) / 1e12
+    dom = max(per_gemm, key=lambda nm: per_gemm[nm]["us"])
+    dd = per_gemm[dom]
+    roofline = {"bound": "mfma", "achieved": round(dd["tflops"], 1), "peak": MFMA_BF16_PEAK,
+                "unit": "TFLOP/s", "frac": round(dd["tflops"] / MFMA_BF16_PEAK, 4), "traffic": None,
+                "kernel": dd["kernel"], "gemm": dom, "launch_us": round(dd["us"], 2)}
+    traffic_file = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(traffic_file):
+        tr = json.load(open(traffic_file)).get(dd["kernel"])
+        if tr:
+            roofline["traffic"] = tr
+
+    result = {
+        "metric": "bf16 GEMM TFLOP/s + % MFMA peak (M=2048); decode matvec HBM GB/s + % peak",
+        "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "4B-class layer prefill GEMMs (qkv, o, gate_up, down) at M=2048 "
+                               "(BASELINE configs[1])", "m": M,
+                   "gemms": {nm: {"k": k, "n": n, "out": ["Bf16", "F32", "Residual"][o],
+                                  "kernel": per_gemm[nm]["kernel"],
+                                  "us": round(per_gemm[nm]["us"], 2),
+                                  "tflops": round(per_gemm[nm]["tflops"], 1)}
+                             for nm, k, n, o in LAYER}},
+        "roofline": roofline,
+    }
+    for b in bufs:
+        g.free(b)
+
+    if not args.no_matvec:
+        result["matvec"] = bench_matvec(g, e, hb)
+    e.log_summary()
+    e.close()
+    g.close()
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(args.cpu_rows)
+    print(json.dumps(result), flush=True)
+
+
+def bench_matvec(g, e, hb):
+    """Decode step at M=1: DECODE_LAYERS layers of the 4 projections plus the
+    lm_head, each weight read once from HBM per step."""
+    out = {}
+    mv_m = 1
+    x_bufs = {}
+    ops, nbytes, tmp = [], 0.0, []
+    for name, k, n, o in LAYER + [LM_HEAD]:
+        layers = 1 if name == "lm_head" else DECODE_LAYERS
+        ws = [g.alloc_with(hb.normal_bf16(0x5EED0003 + 17 * i + n, 0.02, (n, k))) for i in range(layers)]
+        if k not in x_bufs:
+            x_bufs[k] = g.alloc_with(hb.normal_bf16(0x5EED0003, 1.0, (mv_m, k)))
+        y = g.alloc_with(hb.normal_bf16(5, 1.0, (mv_m, n)))
+        tmp += ws + [y]
+        kern = e.mv(k, n, o, mv_m, [hb.r(w) for w in ws], hb.r(x_bufs[k]), hb.r(y))
+        for w in ws:
+            ops.append(hb.Op(kern, [hb.r(w), hb.r(x_bufs[k]), hb.r(y)], mv_m))
+            nbytes += 2.0 * n * k + 2.0 * mv_m * k + 2.0 * mv_m * n * (2 if o == 2 else 1)
+        out[name] = g.kernel_name(kern)
+    g.time_ops(ops, 3)
+    reps = 20
+    t = g.time_ops(ops, reps) / reps
+    gbs = nbytes / t / 1e9
+    # the lm_head alone, two copies in turn (2 x 778 MB: no copy is still in
+    # the 256 MB last-level cache when it is read again)
+    k, n = LM_HEAD[1], LM_HEAD[2]
+    w2 = g.alloc_with(hb.normal_bf16(0x5EED0099, 0.02, (n, k)))
+    tmp.append(w2)
+    head2 = hb.Op(ops[-1].kernel, [hb.r(w2), ops[-1].bind[1], ops[-1].bind[2]], mv_m)
+    th = g.time_ops([ops[-1], head2], reps) / reps / 2
+    hb_bytes = 2.0 * LM_HEAD[1] * LM_HEAD[2] + 2.0 * mv_m * LM_HEAD[1] + 2.0 * mv_m * LM_HEAD[2]
+    for b in tmp + list(x_bufs.values()):
+        g.free(b)
+    return {"value": round(gbs, 1), "unit": "GB/s", "frac": round(gbs / HBM_PEAK, 4),
+            "peak": HBM_PEAK, "ms_per_step": round(t * 1e3, 4),
+            "config": {"m": mv_m, "layers": DECODE_LAYERS, "bytes_per_step": nbytes,
+                       "kernels": out},
+            "lm_head": {"gbs": round(hb_bytes / th / 1e9, 1), "us": round(th * 1e6, 2),
+                        "frac": round(hb_bytes / th / 1e9 / HBM_PEAK, 4)}}
+
+
+if __name__ == "__main__":
+    main()

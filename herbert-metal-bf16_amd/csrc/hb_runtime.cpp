@@ -91,6 +91,7 @@ static int compile(const Emitted& em, const std::string& arch, std::string* code
                                      "-std=c++17", "-Xclang", "-target-feature", "-Xclang",
                                      "-packed-fp32-ops"};
     for (const auto& d : em.defines) opts.push_back(d);
+    opts.push_back("-DHB_NAME=" + em.name);
     // The disk cache: the source, its headers and the options hashed.
     std::string key = text;
     for (const auto& s : kSources) key += s.text;
@@ -169,7 +170,7 @@ static int load_kernel(hb_gpu* g, const hb_desc& d, Kernel* k) {
     if (rc) return rc;
     HB_HIP(hipSetDevice(g->device));
     HB_HIP(hipModuleLoadData(&k->module, code.data()));
-    HB_HIP(hipModuleGetFunction(&k->fn, k->module, "hb_kernel"));
+    HB_HIP(hipModuleGetFunction(&k->fn, k->module, k->em.name.c_str()));
     g->compile_seconds +=
         std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
     return HB_OK;

@@ -33,7 +33,7 @@ HB_DEV void store4(void* Yv, u64 at, float v0, float v1, float v2, float v3) {
     }
 }
 
-extern "C" __global__ __launch_bounds__(NT) void hb_kernel(
+extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     const u32* __restrict__ state, const u16* __restrict__ W, const u16* __restrict__ X,
     void* __restrict__ Yv, const u32* __restrict__ unused0, const u32* __restrict__ unused1,
     u32 m_launch) {

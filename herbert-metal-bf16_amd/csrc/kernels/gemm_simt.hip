@@ -27,7 +27,7 @@ HB_DEV void store1(void* Yv, u64 at, float v) {
     }
 }
 
-extern "C" __global__ __launch_bounds__(256) void hb_kernel(
+extern "C" __global__ __launch_bounds__(256) void HB_NAME(
     const u32* __restrict__ state, const u16* __restrict__ W, const u16* __restrict__ X,
     void* __restrict__ Yv, const u32* __restrict__ unused0, const u32* __restrict__ unused1,
     u32 m_launch) {

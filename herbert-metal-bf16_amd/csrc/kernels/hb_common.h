@@ -75,3 +75,9 @@ HB_DEV u32 xcd_remap(u32 g, u32 groups) {
     const u32 q = groups >> 3, r = groups & 7u;
     return x * q + (x < r ? x : r) + i;
 }
+
+// The kernel's symbol: the emitted name (gemm_mma_2560x4608_..., set with
+// -DHB_NAME by the library), so profiles tell the variants apart.
+#ifndef HB_NAME
+#define HB_NAME hb_kernel
+#endif

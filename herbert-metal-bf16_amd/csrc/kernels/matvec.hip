@@ -65,7 +65,7 @@ HB_DEV float wave_sum(float v) {
     return v;
 }
 
-extern "C" __global__ __launch_bounds__(NT) void hb_kernel(const u16* __restrict__ W,
+extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__ W,
                                                            const u16* __restrict__ x,
                                                            void* __restrict__ y, u32 m_launch) {
     __shared__ float part[SPLIT > 1 ? WAVES * RB * 16 : 1];

@@ -27,7 +27,7 @@ constexpr u32 E = HB_E, TOPK = HB_TOPK, D = HB_D;
 static_assert(E % 64 == 0 && E <= 1024 && TOPK <= 64, "route: experts a multiple of 64");
 constexpr u32 P = E / 64;
 
-extern "C" __global__ __launch_bounds__(256) void hb_kernel(const u16* __restrict__ scores,
+extern "C" __global__ __launch_bounds__(256) void HB_NAME(const u16* __restrict__ scores,
                                                             u32* __restrict__ route, u32 rows) {
     const u32 lane = threadIdx.x & 63u;
     const u32 r = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -107,7 +107,7 @@ extern "C" __global__ __launch_bounds__(256) void hb_kernel(const u16* __restric
 static_assert(E <= 1024, "sort: at most 1024 experts");
 constexpr u32 BM = HB_BM, NW = 16;
 
-extern "C" __global__ __launch_bounds__(1024) void hb_kernel(const u32* __restrict__ state,
+extern "C" __global__ __launch_bounds__(1024) void HB_NAME(const u32* __restrict__ state,
                                                              const u32* __restrict__ route,
                                                              u32* __restrict__ list,
                                                              u32* __restrict__ tiles, u32 m_launch) {
@@ -206,7 +206,7 @@ extern "C" __global__ __launch_bounds__(1024) void hb_kernel(const u32* __restri
 static_assert(D % 8 == 0, "gather: hidden a multiple of 8");
 constexpr u32 CELLS = D / 8;
 
-extern "C" __global__ __launch_bounds__(256) void hb_kernel(const u32* __restrict__ state,
+extern "C" __global__ __launch_bounds__(256) void HB_NAME(const u32* __restrict__ state,
                                                             const u32* __restrict__ list,
                                                             const u32x4* __restrict__ X,
                                                             u32x4* __restrict__ XS, u32 m_launch) {
@@ -225,7 +225,7 @@ extern "C" __global__ __launch_bounds__(256) void hb_kernel(const u32* __restric
 static_assert(D % 8 == 0, "swiglu: n a multiple of 8");
 constexpr u32 CELLS = D / 8;
 
-extern "C" __global__ __launch_bounds__(256) void hb_kernel(const u32x4* __restrict__ gu,
+extern "C" __global__ __launch_bounds__(256) void HB_NAME(const u32x4* __restrict__ gu,
                                                             u32x4* __restrict__ h, u32 rows) {
     const u64 i = (u64)blockIdx.x * 256 + threadIdx.x;
     if (i >= (u64)rows * CELLS) return;
@@ -249,7 +249,7 @@ extern "C" __global__ __launch_bounds__(256) void hb_kernel(const u32x4* __restr
 static_assert(D % 8 == 0, "combine: hidden a multiple of 8");
 constexpr u32 CELLS = D / 8;
 
-extern "C" __global__ __launch_bounds__(256) void hb_kernel(const u32x4* __restrict__ y,
+extern "C" __global__ __launch_bounds__(256) void HB_NAME(const u32x4* __restrict__ y,
                                                             const u32* __restrict__ route,
                                                             u32x4* __restrict__ out, u32 rows) {
     const u64 i = (u64)blockIdx.x * 256 + threadIdx.x;
