@@ -70,9 +70,15 @@ int emit(const hb_desc& d, Emitted* e) {
             e->threads = 256;
             e->nbind = 1;
             return HB_OK;
-        case HB_KIND_GEMM: {
+        case HB_KIND_GEMM:
+        case HB_KIND_GEMM_SWIGLU: {
+            const bool swi = d.kind == HB_KIND_GEMM_SWIGLU;
             if (d.rows_of > HB_ROWS_SORTED || d.out > HB_OUT_RESIDUAL)
                 return fail(HB_ERR_INVALID, "gemm: rows_of/out out of range");
+            if (swi && (d.rows_of != HB_ROWS_DENSE || d.out != HB_OUT_BF16))
+                return fail(HB_ERR_UNSUPPORTED, "gemm_swiglu: dense rows, bf16 out");
+            if (d.band && d.rows_of != HB_ROWS_DENSE)
+                return fail(HB_ERR_UNSUPPORTED, "gemm: band order over dense rows only");
             if (d.mfma != 16 && d.mfma != 32) return fail(HB_ERR_UNSUPPORTED, "gemm: mfma 16 or 32");
             if (!d.k || !d.n || d.k % d.bk || d.n % 4 || !pow2(d.bk) || d.bk < 32)
                 return fail(HB_ERR_UNSUPPORTED, "gemm " + std::to_string(d.k) + "x" +
@@ -81,6 +87,9 @@ int emit(const hb_desc& d, Emitted* e) {
             if (!d.wm || !d.wn || d.wm * d.wn > 16 || d.bm % (d.wm * d.mfma) ||
                 d.bn % (d.wn * d.mfma))
                 return fail(HB_ERR_UNSUPPORTED, "gemm: tile not a multiple of waves x mfma");
+            if (swi && (d.bn / (d.wn * d.mfma)) % 2)
+                return fail(HB_ERR_UNSUPPORTED,
+                            "gemm_swiglu: an even count of W fragments per wave (bn / (wn * mfma))");
             bool experts = d.rows_of != HB_ROWS_DENSE;
             if (experts && (!d.top_k || !d.experts || !d.tiles))
                 return fail(HB_ERR_INVALID, "gemm over experts: top_k, experts and tiles");
@@ -105,11 +114,11 @@ int emit(const hb_desc& d, Emitted* e) {
             }
             if (d.dbuf > 3 || (!d.lds_dma && d.dbuf > 1))
                 return fail(HB_ERR_UNSUPPORTED, "gemm: stages 1..4 (1..2 through registers)");
-            if (d.lds_dma && ((d.bm * d.bk / 8) % e->threads || (d.bn * d.bk / 8) % e->threads))
-                return fail(HB_ERR_UNSUPPORTED, "gemm: direct-to-LDS staging needs whole chunks per lane");
-            snprintf(name, sizeof name, "gemm_mma_%ux%u_%s%s_t%ux%u_k%u_w%ux%u_x%u_d%u%s_s%u_o%u%s",
-                     d.k, d.n, out_tag(d.out), d.m_first ? "_mf" : "", d.bn, d.bm, d.bk, d.wn, d.wm,
-                     d.mfma, d.dbuf, d.lds_dma ? "_dma" : "", shift, d.order, rows.c_str());
+            std::string band = d.band ? "_b" + std::to_string(d.band) : "";
+            snprintf(name, sizeof name, "gemm_mma%s_%ux%u_%s%s_t%ux%u_k%u_w%ux%u_x%u_d%u%s_s%u_o%u%s%s",
+                     swi ? "_swiglu" : "", d.k, d.n, out_tag(d.out), d.m_first ? "_mf" : "", d.bn,
+                     d.bm, d.bk, d.wn, d.wm, d.mfma, d.dbuf, d.lds_dma ? "_dma" : "", shift, d.order,
+                     band.c_str(), rows.c_str());
             e->name = name;
             e->source = "gemm_mfma.hip";
             e->threads = 64 * d.wm * d.wn;
@@ -120,7 +129,8 @@ int emit(const hb_desc& d, Emitted* e) {
                           D("HB_WM", d.wm),      D("HB_WN", d.wn),     D("HB_MFMA", d.mfma),
                           D("HB_STAGES", d.dbuf + 1), D("HB_SWZ", shift),
                           D("HB_ORDER", d.order), D("HB_MFIRST", d.m_first ? 1 : 0),
-                          D("HB_DMA", d.lds_dma ? 1 : 0)};
+                          D("HB_DMA", d.lds_dma ? 1 : 0), D("HB_SWIGLU", swi ? 1 : 0),
+                          D("HB_BAND", d.band)};
             return HB_OK;
         }
         case HB_KIND_GEMM_SIMT:
@@ -241,7 +251,8 @@ uint32_t groups_of(const hb_desc& d, uint32_t m) {
         case HB_KIND_GEMM_SIMT:
         case HB_KIND_GEMM_SWIGLU: {
             uint32_t bm = d.kind == HB_KIND_GEMM_SIMT ? 64 : d.bm;
-            uint32_t nt = cdiv(d.n, d.kind == HB_KIND_GEMM_SIMT ? 64 : d.bn);
+            uint32_t bn = d.kind == HB_KIND_GEMM_SIMT ? 64 : d.kind == HB_KIND_GEMM_SWIGLU ? d.bn / 2 : d.bn;
+            uint32_t nt = cdiv(d.n, bn);
             if (d.rows_of != HB_ROWS_DENSE) return d.tiles * nt;  // gemm_mma_expert_groups
             return cdiv(m, bm) * nt;                                 // gemm_mma_groups
         }

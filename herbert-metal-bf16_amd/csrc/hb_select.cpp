@@ -232,7 +232,7 @@ struct Tune {
 // indexes this table (gemm.mma=1).
 struct Form {
     const char* name;
-    uint32_t bm, bn, bk, wm, wn, mfma, dbuf, dma, order;
+    uint32_t bm, bn, bk, wm, wn, mfma, dbuf, dma, order, band;
 };
 const Form kForms[10] = {
     {"mma", 128, 128, 64, 2, 2, 16, 1, 1, 1},
@@ -245,6 +245,23 @@ const Form kForms[10] = {
     {"mma_k32_s4", 128, 128, 32, 2, 2, 16, 3, 1, 1},
     {"mma_reg", 128, 128, 64, 2, 2, 16, 1, 0, 0},
     {"mma_t64", 64, 64, 32, 1, 4, 16, 0, 0, 0},
+};
+// Timed with the table but not named by gemm.mform: tiles whose counts
+// fill whole rounds of the 256 CUs on this build's shapes (256 x 192:
+// 768 tiles at 2048 x 18432; 128 x 160: 256 at 2048 x 2560), and the
+// band tile order of gemm_nax (prefill.rs:615-631).
+const Form kMoreForms[] = {
+    {"mma_t256x192_w8", 256, 192, 64, 4, 2, 32, 1, 1, 1},
+    {"mma_t128x160", 128, 160, 64, 2, 2, 16, 1, 1, 1},
+    {"mma_b2", 128, 128, 64, 2, 2, 16, 1, 1, 0, 2},
+};
+// The fused [gate | up] + SwiGLU forms (gate_up_pipes, qwen.rs:2148-2193):
+// bn W rows per tile = bn/2 features.
+const Form kFusedForms[] = {
+    {"fused128x64", 128, 128, 64, 2, 2, 16, 1, 1, 1},
+    {"fused128x64b2", 128, 128, 64, 2, 2, 16, 1, 1, 0, 2},
+    {"fused256x96", 256, 192, 64, 4, 2, 16, 1, 1, 1},
+    {"fused256x128", 256, 256, 64, 4, 2, 32, 1, 1, 1},
 };
 
 hb_desc form_desc(const Form& f, uint32_t k, uint32_t n, uint32_t out, bool mf) {
@@ -264,6 +281,7 @@ hb_desc form_desc(const Form& f, uint32_t k, uint32_t n, uint32_t out, bool mf) 
     d.dbuf = f.dbuf;
     d.lds_dma = f.dma;
     d.order = f.order;
+    d.band = f.band;
     return d;
 }
 
@@ -305,6 +323,7 @@ struct hb_engine {
     Tune t;
     std::string tune_summary, log;
     std::map<std::string, int32_t> gemm_pick;
+    std::map<std::string, std::pair<int32_t, int32_t>> gate_up_pick;
     std::map<std::string, hb_desc> mv_pick;
     std::vector<std::pair<std::string, hb_desc>> extra;  // hb_engine_add_gemm_candidate
     double autotune_seconds = 0.0;
@@ -575,6 +594,7 @@ int hb_engine_gemm(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, hb_range 
     for (const auto& f : kForms) add(f.name, form_desc(f, k, n, out, mf));
     if (c.empty() || c[0].name != "mma")
         return fail(HB_ERR_COMPILE, what + ": the production kernel mma is not built: " + hb_last_error());
+    for (const auto& f : kMoreForms) add(f.name, form_desc(f, k, n, out, mf));
     for (auto tm_tn : {std::make_pair(64u, 64u), std::make_pair(64u, 32u), std::make_pair(32u, 64u),
                        std::make_pair(32u, 32u), std::make_pair(64u, 16u), std::make_pair(32u, 16u)}) {
         char nm[32];
@@ -592,6 +612,62 @@ int hb_engine_gemm(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, hb_range 
     e->gemm_pick[key] = c[best].kernel;
     *kernel = c[best].kernel;
     return HB_OK;
+}
+
+int hb_engine_gate_up(hb_engine* e, uint32_t h, uint32_t inter, hb_range state, hb_range w,
+                      hb_range x, hb_range gu, hb_range hout, uint32_t m, int32_t* gemm_kernel,
+                      int32_t* swiglu_kernel) {
+    const Tune& t = e->t;
+    int rc;
+    *gemm_kernel = *swiglu_kernel = -1;
+    char key[128];
+    snprintf(key, sizeof key, "%ux%u, %u rows", h, 2 * inter, m);
+    auto it = e->gate_up_pick.find(key);
+    if (it != e->gate_up_pick.end()) {
+        *gemm_kernel = it->second.first;
+        *swiglu_kernel = it->second.second;
+        return HB_OK;
+    }
+    int32_t gk, sk;
+    if ((rc = hb_engine_gemm(e, h, 2 * inter, HB_OUT_BF16, state, w, x, gu, m, &gk))) return rc;
+    hb_desc sd{};
+    sd.kind = HB_KIND_SWIGLU;
+    sd.n = inter;
+    if ((rc = e->build(sd, &sk))) return rc;
+    const bool timed = t["gemm.auto"] && !t.gemm_set;
+    const uint32_t fswi = t["pf.fswi"];
+    auto keep = [&](int32_t a, int32_t b) {
+        e->gate_up_pick[key] = {a, b};
+        *gemm_kernel = a;
+        *swiglu_kernel = b;
+        return HB_OK;
+    };
+    if (fswi == 0 || (fswi == 2 && !timed) || h % 32) return keep(gk, sk);
+    bool mf = t["gemm.mfirst"] != 0;
+    std::string what = std::string("gate_up+swiglu ") + key;
+    std::vector<Cand> c;
+    std::vector<bool> eligible;
+    if (fswi == 2) {
+        c.push_back({"apart", gk, {make_op(gk, m, {state, w, x, gu, state, state}), make_op(sk, m, {gu, hout})}});
+        eligible.push_back(true);
+    }
+    for (const auto& f : kFusedForms) {
+        hb_desc d = form_desc(f, h, inter, HB_OUT_BF16, mf);
+        d.kind = HB_KIND_GEMM_SWIGLU;
+        int32_t kk;
+        if (e->build(d, &kk)) {
+            e->logf("[autotune] gate_up+swiglu: %s not built (%s)", f.name, hb_last_error());
+            continue;
+        }
+        c.push_back({f.name, kk, {make_op(kk, m, {state, w, x, hout, state, state})}});
+        eligible.push_back(true);
+    }
+    if (c.empty()) return keep(gk, sk);
+    if (fswi == 1) return c[0].name == "apart" ? keep(gk, sk) : keep(c[0].kernel, -1);
+    if ((rc = e->check_candidates(what, c, eligible, state, hout, false, m, inter * 2))) return rc;
+    size_t best;
+    if ((rc = e->pick_flagged(what, c, eligible, &best, nullptr))) return rc;
+    return best == 0 ? keep(gk, sk) : keep(c[best].kernel, -1);
 }
 
 int hb_engine_matvec(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, uint32_t mv_m,

@@ -35,7 +35,16 @@
 // residual), HB_ROWS (0 dense, 1 gather, 2 scatter, 3 sorted: row p of X
 // and of Y, the rows a gather put in sorted order), HB_TOPK, HB_BM, HB_BN,
 // HB_BK, HB_WM, HB_WN, HB_MFMA (16|32), HB_STAGES (1..4), HB_SWZ, HB_ORDER,
-// HB_MFIRST, HB_DMA.
+// HB_MFIRST, HB_DMA, HB_SWIGLU, HB_BAND (the tile order band).
+//
+// HB_SWIGLU 1 (dense rows, Bf16): the [gate | up] projection and the SwiGLU
+// in one (prefill.rs:755-824, gemm_nax_swiglu).  N is the feature count nf
+// and W holds 2*nf rows (gate rows, then their up rows); a tile covers BN/2
+// features: each wave's W fragments 0..IN/2-1 are gate rows and fragments
+// IN/2.. the up rows of the same features, so a lane holds the gate and the
+// up sums of the same outputs and writes h = rne(g * sigmoid(g) * u) with g,
+// u the bf16-rounded sums -- the bits of the unfused GEMM (same tile form)
+// followed by swiglu_rows, since each sum runs the same MFMA sequence.
 //
 // Bindings: state (u32[4], state[3] = rows), W, X, Y, list, tiles; then the
 // rows the launch was sized for (m_launch).  Dense: rows past m read the
@@ -55,9 +64,21 @@ constexpr u32 CH = BK / 8;                  // 16-byte chunks of a staged row
 constexpr u32 KS = FM == 16 ? 32 : 16;      // K of one MFMA
 constexpr u32 S = BK / KS;                  // MFMA steps per staged tile
 constexpr u32 KT = K / BK;
-constexpr u32 NTILES = (N + BN - 1) / BN;
+#ifndef HB_SWIGLU
+#define HB_SWIGLU 0
+#endif
+#ifndef HB_BAND
+#define HB_BAND 0
+#endif
+constexpr bool SWI = HB_SWIGLU != 0;
+constexpr u32 BF = SWI ? BN / 2 : BN;       // output columns of a tile
+constexpr u32 NTILES = (N + BF - 1) / BF;
 constexpr u32 XCH = BM * CH, WCH = BN * CH;  // chunks per stage
 constexpr u32 X_LD = (XCH + NT - 1) / NT, W_LD = (WCH + NT - 1) / NT;
+// Direct-to-LDS staging writes whole wavefronts of chunks: the stage is
+// padded to a multiple of the workgroup's lanes (the padding holds copies of
+// the tile's last row, never read), so every wave issues the same loads.
+constexpr u32 XCHP = HB_DMA ? X_LD * NT : XCH, WCHP = HB_DMA ? W_LD * NT : WCH;
 constexpr u32 NS = HB_STAGES;
 
 static_assert(K % BK == 0, "K a multiple of the K step");
@@ -66,9 +87,9 @@ static_assert(TM % FM == 0 && TN % FM == 0, "wave tile a multiple of the MFMA bl
 static_assert(BK % KS == 0 && (CH & (CH - 1)) == 0, "K step");
 static_assert(NT % CH == 0, "threads a multiple of the chunks of a row");
 static_assert(NS >= 1 && NS <= 4, "1 to 4 stages");
-static_assert(!HB_DMA || (XCH % NT == 0 && WCH % NT == 0),
-              "direct-to-LDS staging: every lane loads the same number of chunks");
 static_assert(HB_DMA || NS <= 2, "register staging: 1 or 2 stages");
+static_assert(!SWI || (IN % 2 == 0 && OUT == 0 && ROWS == 0),
+              "fused SwiGLU: dense rows, bf16 out, an even count of W fragments per wave");
 
 typedef __attribute__((ext_vector_type(FM == 16 ? 4 : 16))) float acc_t;
 
@@ -122,10 +143,10 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     u32 m_launch) {
     // The stages as distinct LDS objects, so that the compiler sees that one
     // stage's direct-to-LDS loads never alias another stage's reads.
-    __shared__ u32x4 sX0[XCH], sW0[WCH];
-    __shared__ u32x4 sX1[NS > 1 ? XCH : 1], sW1[NS > 1 ? WCH : 1];
-    __shared__ u32x4 sX2[NS > 2 ? XCH : 1], sW2[NS > 2 ? WCH : 1];
-    __shared__ u32x4 sX3[NS > 3 ? XCH : 1], sW3[NS > 3 ? WCH : 1];
+    __shared__ u32x4 sX0[XCHP], sW0[WCHP];
+    __shared__ u32x4 sX1[NS > 1 ? XCHP : 1], sW1[NS > 1 ? WCHP : 1];
+    __shared__ u32x4 sX2[NS > 2 ? XCHP : 1], sW2[NS > 2 ? WCHP : 1];
+    __shared__ u32x4 sX3[NS > 3 ? XCHP : 1], sW3[NS > 3 ? WCHP : 1];
 #define STX(i) ((i) == 0 ? sX0 : (i) == 1 ? sX1 : (i) == 2 ? sX2 : sX3)
 #define STW(i) ((i) == 0 ? sW0 : (i) == 1 ? sW1 : (i) == 2 ? sW2 : sW3)
 
@@ -142,7 +163,23 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
         const u32 m = rows_of_state(state, m_launch);
         const u32 mb = (m + BM - 1) / BM;
         u32 gm;
-        if (HB_MFIRST) { gm = g % mb; gn = g / mb; }
+        if constexpr (HB_BAND > 0) {
+            // nax_tile_order (prefill.rs:615-631): bands of HB_BAND row
+            // tiles, each walked over every column tile, its row tiles
+            // interleaved; the last band holds the rest.
+            constexpr u32 PER = HB_BAND * NTILES;
+            const u32 full = mb / HB_BAND;
+            if (g < full * PER) {
+                const u32 idx = g % PER;
+                gm = (g / PER) * HB_BAND + idx % HB_BAND;
+                gn = idx / HB_BAND;
+            } else {
+                const u32 rem = mb - full * HB_BAND, idx = g - full * PER;
+                if (rem == 0) return;  // groups past m's tiles
+                gm = full * HB_BAND + idx % rem;
+                gn = idx / rem;
+            }
+        } else if (HB_MFIRST) { gm = g % mb; gn = g / mb; }
         else { gn = g % NTILES; gm = g / NTILES; }
         if (gm >= mb || gn >= NTILES) return;
         row0 = gm * BM;
@@ -158,7 +195,7 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
         rows = tiles[3 + 3 * t];
     }
     const u32 pairs = m_launch * TOPK;  // experts: sorted rows of the block
-    const u32 n0 = gn * BN;
+    const u32 n0 = gn * BF;
 
     // Global element offsets of this thread's chunks (row clamped to the
     // last valid one), advanced by BK per K tile.  Register staging: chunk
@@ -181,6 +218,14 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     };
     auto w_row = [&](u32 r) HB_INLINE -> u32 {
         if (r >= BN) r = BN - 1;
+        if constexpr (SWI) {
+            // Tile row r: wave r / TN, its fragment i; gate rows for i <
+            // IN/2, else the up rows of fragment i - IN/2's features.
+            const u32 t = r % TN, i = t / FM, up = i >= IN / 2 ? 1u : 0u;
+            u32 f = n0 + (r / TN) * (TN / 2) + (i - up * (IN / 2)) * FM + t % FM;
+            f = f < N ? f : N - 1;
+            return up * N + f;
+        }
         u32 n = n0 + r;
         return expert * N + (n < N ? n : N - 1);
     };
@@ -397,6 +442,27 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
             yrow = s < pairs ? s : pairs - 1;
         } else {
             yrow = row0 + ml;
+        }
+        if constexpr (SWI) {
+#pragma unroll
+            for (u32 i = 0; i < IN / 2; i++) {
+#pragma unroll
+                for (u32 q = 0; q < FM * FM / 256; q++) {
+                    const u32 f = n0 + wn * (TN / 2) + i * FM + q * 8 + 4 * fc;
+                    if (f < N) {
+                        const acc_t& g = acc[i][j];
+                        const acc_t& u = acc[i + IN / 2][j];
+                        float h[4];
+#pragma unroll
+                        for (u32 e = 0; e < 4; e++) {
+                            const float gr = round_bf16(g[4 * q + e]), ur = round_bf16(u[4 * q + e]);
+                            h[e] = (gr * hb_sigmoid(gr)) * ur;
+                        }
+                        store4(Yv, (u64)yrow * N + f, h[0], h[1], h[2], h[3]);
+                    }
+                }
+            }
+            continue;
         }
 #pragma unroll
         for (u32 i = 0; i < IN; i++) {

@@ -94,12 +94,12 @@ class Range(ctypes.Structure):
 
 _DESC_FIELDS = ["kind", "k", "n", "out", "rows_of", "m_first", "bm", "bn", "bk", "wm", "wn",
                 "mfma", "dbuf", "swz", "order", "mv_m", "split", "persist", "rows", "form",
-                "top_k", "experts", "tiles", "rows_max", "lds_dma", "unroll"]
+                "top_k", "experts", "tiles", "rows_max", "lds_dma", "unroll", "band"]
 
 
 class Desc(ctypes.Structure):
     """hb_desc: a kernel's shape-keyed descriptor (what an emitter fixes)."""
-    _fields_ = [(f, ctypes.c_uint32) for f in _DESC_FIELDS] + [("reserved", ctypes.c_uint32 * 6)]
+    _fields_ = [(f, ctypes.c_uint32) for f in _DESC_FIELDS] + [("reserved", ctypes.c_uint32 * 5)]
 
     def __init__(self, **kw):
         super().__init__()
@@ -172,6 +172,8 @@ lib.hb_engine_tune_summary.restype = ctypes.c_char_p
 lib.hb_engine_buckets.argtypes = [_P, ctypes.POINTER(_u32), _u32, ctypes.POINTER(_u32)]
 lib.hb_engine_gemm.argtypes = [_P, _u32, _u32, _u32, Range, Range, Range, Range, _u32,
                                ctypes.POINTER(_i32)]
+lib.hb_engine_gate_up.argtypes = [_P, _u32, _u32, Range, Range, Range, Range, Range, _u32,
+                                  ctypes.POINTER(_i32), ctypes.POINTER(_i32)]
 lib.hb_engine_matvec.argtypes = [_P, _u32, _u32, _u32, _u32, ctypes.POINTER(Range), _u32, Range,
                                  Range, ctypes.POINTER(_i32)]
 lib.hb_engine_experts.argtypes = [_P, _u32, _u32, _u32, _u32, _u32, ctypes.POINTER(MoeIo),
@@ -238,6 +240,17 @@ def gemm_mm2d(kdim, n, out, tm=64, tn=64, m_first=True):
 def gemm_mma(kdim, n, out, m_first=True, **tile):
     """gemm_mma (prefill.rs:418): the dense MFMA GEMM."""
     return gemm_mma_rows(kdim, n, out, m_first, Rows.Dense, **tile)
+
+
+def gemm_mma_swiglu(kdim, nf, m_first=True, **tile):
+    """gemm_nax_swiglu (prefill.rs:755-824): W [2*nf][K] (gate rows, then up rows),
+    H [m][nf] = rne(g * sigmoid(g) * u) of the bf16-rounded sums, in one MFMA GEMM."""
+    return Desc(kind=Kind.GEMM_SWIGLU, k=kdim, n=nf, out=Out.Bf16, m_first=m_first, **tile)
+
+
+def swiglu_rows(nf):
+    """swiglu_rows (prefill.rs:2790) / swiglu_slots: H[r] from the row's [gate | up]."""
+    return Desc(kind=Kind.SWIGLU, n=nf)
 
 
 def matvec(kdim, n, out, mv_m=1, rows=4, split=1, persist=0, form=0, unroll=4):
@@ -407,6 +420,13 @@ class Engine:
         kern = _i32()
         check(lib.hb_engine_gemm(self.h, k, n, int(out), state, w, x, y, m, ctypes.byref(kern)))
         return kern.value
+
+    def gate_up(self, h, inter, state, w, x, gu, hout, m):
+        """gate_up_pipes (qwen.rs:2148): (GEMM or fused kernel, SwiGLU kernel or -1)."""
+        a, b = _i32(), _i32()
+        check(lib.hb_engine_gate_up(self.h, h, inter, state, w, x, gu, hout, m, ctypes.byref(a),
+                                    ctypes.byref(b)))
+        return a.value, b.value
 
     def mv(self, k, n, out, mv_m, ws, x, y):
         arr = (Range * len(ws))(*ws)

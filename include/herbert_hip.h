@@ -118,7 +118,12 @@ typedef struct hb_desc {
     /* matvec: 16-byte chunks (VALU form) or 32-K MFMA steps (MFMA form)
      * each lane keeps in flight per row; 0 = 4. */
     uint32_t unroll;
-    uint32_t reserved[6];
+    /* GEMM tile order band (nax_tile_order, prefill.rs:615-631): 0 the
+     * m_first walk; b > 0: consecutive workgroups walk every column tile of
+     * b row tiles, those row tiles interleaved (the last band holds what is
+     * left).  Dense rows only. */
+    uint32_t band;
+    uint32_t reserved[5];
 } hb_desc;
 
 /* Gpu::pipeline(&Emitted) (metal/gpu.rs:127-148) for the kernel the
@@ -192,6 +197,19 @@ int hb_engine_buckets(hb_engine *engine, uint32_t *out, uint32_t cap, uint32_t *
  * timed on (state[3] and Y restored afterwards).  Logs [autotune] lines. */
 int hb_engine_gemm(hb_engine *engine, uint32_t k, uint32_t n, uint32_t out, hb_range state,
                    hb_range w, hb_range x, hb_range y, uint32_t m, int32_t *kernel);
+
+/* QwenEngine::gate_up_pipes (qwen.rs:2148-2193): the prefill's [gate | up]
+ * GEMM (K = h, N = 2*inter, Bf16 into `gu`) and its SwiGLU into `hout`
+ * ([m][inter]).  pf.fswi 0: apart; 1: the first fused form
+ * (gemm_nax_swiglu, prefill.rs:755-824); 2 (default, with gemm.auto): the
+ * GEMM's pick + swiglu_rows timed against the fused forms after
+ * check_candidates, the fastest kept under "{h}x{2 inter}, {m} rows".
+ * *gemm_kernel: the GEMM (bindings state, W, X, gu) or the fused kernel
+ * (state, W, X, hout); *swiglu_kernel: the SwiGLU (bindings gu, hout) or
+ * -1 when fused. */
+int hb_engine_gate_up(hb_engine *engine, uint32_t h, uint32_t inter, hb_range state, hb_range w,
+                      hb_range x, hb_range gu, hb_range hout, uint32_t m, int32_t *gemm_kernel,
+                      int32_t *swiglu_kernel);
 
 /* QwenEngine::mv_full (qwen.rs:1311-1511) for M rows of x: with mv.auto the
  * forms timed over every matrix of the shape (`ws`, mv.cold) and the fastest

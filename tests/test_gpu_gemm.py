@@ -20,6 +20,10 @@ TILES = {
     "t256x128_d4": dict(bm=128, bn=256, bk=32, wm=2, wn=2, mfma=32, dbuf=3, lds_dma=1, order=1),
     "t128x128_reg_d1": dict(bm=128, bn=128, bk=64, wm=2, wn=2, mfma=16, dbuf=1, lds_dma=0, order=0),
     "t64x64_reg_s1": dict(bm=64, bn=64, bk=32, wm=1, wn=4, mfma=16, dbuf=0, lds_dma=0, order=0),
+    "t256x192_w8_x32": dict(bm=256, bn=192, bk=64, wm=4, wn=2, mfma=32, dbuf=1, lds_dma=1, order=1),
+    "t128x160_x16": dict(bm=128, bn=160, bk=64, wm=2, wn=2, mfma=16, dbuf=1, lds_dma=1, order=1),
+    "t128x128_band2": dict(bm=128, bn=128, bk=64, wm=2, wn=2, mfma=16, dbuf=1, lds_dma=1, order=0,
+                           band=2),
 }
 
 
@@ -89,6 +93,19 @@ def test_gemm_state_rows_below_launch_rows(gpu):
         gpu.free(b)
     assert np.all(got[100:] == 0)
     check_close(got[:100], orc.gemm(x[:100], w), k, abs_products(x[:100], w), "state rows")
+
+
+@pytest.mark.parametrize("band", [1, 2, 3])
+def test_gemm_band_order_covers_every_tile(gpu, band):
+    """nax_tile_order's bands (prefill.rs:615-631) with a last band shorter
+    than the others (5 row tiles): same output as the m_first walk, bit for
+    bit, every row written."""
+    m, k, n = 600, 256, 1000
+    x, w = inputs(m, k, n, 13)
+    base = dict(TILES["t128x128_x16_d2"], order=0)
+    want = run_gemm(gpu, x, w, 0, **base)
+    got = run_gemm(gpu, x, w, 0, np.full((m, n), 0x7FC1, np.uint16), band=band, **base)
+    assert np.array_equal(got, want)
 
 
 LAYER4B = [("qkv", 2560, 4608, 0), ("o", 4096, 2560, 2), ("gate_up", 2560, 18432, 0),
