@@ -16,6 +16,19 @@ streamed per step, as GB/s of algorithmic bytes (2*N*K + 2*M*K + 2*M*N per
 projection, + 2*M*N for Residual) against HBM's 8 TB/s.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--tune key=value,...]
+
+roofline.traffic (HBM bytes per launch of the dominant kernel) comes from
+profiles/traffic.json, written from two counter runs of this file:
+
+    rocprofv3 --pmc FETCH_SIZE -d F -o run --output-format csv -- python3 bench.py --traffic-run
+    rocprofv3 --pmc WRITE_SIZE -d W -o run --output-format csv -- python3 bench.py --traffic-run
+    python3 bench.py --traffic-summary F/run_counter_collection.csv W/run_counter_collection.csv
+
+--traffic-run selects the step's kernels (every candidate is dispatched, so
+every candidate gets counters) and copies COPY_BYTES device to device; the
+summary scales each kernel's FETCH_SIZE and WRITE_SIZE (KiB per dispatch)
+by what the same counter reads for that copy (COPY_BYTES read, COPY_BYTES
+written).
 """
 import argparse
 import json
@@ -36,6 +49,7 @@ LAYER = [("qkv", 2560, 4608, 0), ("o", 4096, 2560, 2), ("gate_up", 2560, 18432, 
 LM_HEAD = ("lm_head", 2560, 151936, 0)
 DECODE_LAYERS = 4
 SEED = 0x5EED0002  # config 2's seeds: X = SEED + 2i, W = SEED + 2i + 1
+COPY_BYTES = 1 << 28  # the calibration copy of the traffic counters
 
 
 def log(*a):
@@ -72,7 +86,12 @@ def main():
     ap.add_argument("--cpu-rows", type=int, default=1536)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-matvec", action="store_true")
+    ap.add_argument("--traffic-run", action="store_true")
+    ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     args = ap.parse_args()
+    if args.traffic_summary:
+        traffic_summary(*args.traffic_summary)
+        return
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only (--gpus %d asked); the path would shard "
               "each GEMM by N across GPUs, which is not built" % args.gpus, file=sys.stderr)
@@ -97,21 +116,24 @@ def main():
         flops += f
         per_gemm[name] = {"kernel": g.kernel_name(kern), "flops": f, "op": op}
     log("[bench] selection done in %.1f s" % (time.time() - t0))
+    if args.traffic_run:
+        traffic_run(g, ops, per_gemm)
+        return
 
-    # Warmup, then exactly K steps between two synchronisations.
+    # Warmup, then exactly K steps between two synchronisations, an event
+    # after every launch: the step time and each GEMM's mean launch time
+    # come from the same timed region.
     g.time_ops(ops, max(args.warmup, 0)) if args.warmup > 0 else None
     g.sync()
-    t = g.time_ops(ops, args.steps)
+    t, each = g.time_each(ops, args.steps)
     g.sync()
     ms = t / args.steps * 1e3
     value = flops / (t / args.steps) / 1e12
 
-    # Per-GEMM kernel time (HIP events on the library's stream), the dominant
-    # kernel's roofline.
-    for name, d in per_gemm.items():
-        reps = 20
-        d["us"] = g.time_ops([d["op"]], reps) / reps * 1e6
-        d["tflops"] = d["flops"] / (d["us"] * 1e-6) / 1e12
+    # The dominant kernel's roofline.
+    for (name, d), s in zip(per_gemm.items(), each):
+        d["us"] = s * 1e6
+        d["tflops"] = d["flops"] / s / 1e12
     dom = max(per_gemm, key=lambda nm: per_gemm[nm]["us"])
     dd = per_gemm[dom]
     roofline = {"bound": "mfma", "achieved": round(dd["tflops"], 1), "peak": MFMA_BF16_PEAK,
@@ -121,7 +143,7 @@ def main():
     if os.path.exists(traffic_file):
         tr = json.load(open(traffic_file)).get(dd["kernel"])
         if tr:
-            roofline["traffic"] = tr
+            roofline["traffic"] = tr["bytes"]
 
     result = {
         "metric": "bf16 GEMM TFLOP/s + % MFMA peak (M=2048); decode matvec HBM GB/s + % peak",
@@ -148,6 +170,64 @@ def main():
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_rows)
     print(json.dumps(result), flush=True)
+
+
+def traffic_run(g, ops, per_gemm):
+    """The picked kernels a few times, then the calibration copy (a device
+    to device copy of COPY_BYTES, HIP's blit kernel)."""
+    import herbert_hip as hb
+    g.time_ops(ops, 3)
+    g.sync()
+    a, b = g.alloc(COPY_BYTES), g.alloc(COPY_BYTES)
+    g.zero(a)
+    for _ in range(5):
+        g.copy(hb.r(b), hb.r(a))
+    g.sync()
+    g.free(a)
+    g.free(b)
+    print(json.dumps({"picked": {nm: d["kernel"] for nm, d in per_gemm.items()},
+                      "copy_bytes": COPY_BYTES}), flush=True)
+
+
+def traffic_summary(fetch_csv, write_csv):
+    """profiles/traffic.json: per kernel (its dispatches over the most
+    workgroups, i.e. the full M=2048 block), the median FETCH_SIZE and
+    WRITE_SIZE scaled by the calibration copy, in bytes per launch."""
+    import csv
+    import statistics
+
+    def per_kernel(path, counter):
+        rows = {}
+        for r in csv.DictReader(open(path)):
+            if r["Counter_Name"] != counter:
+                continue
+            rows.setdefault(r["Kernel_Name"], []).append((int(r["Grid_Size"]), float(r["Counter_Value"])))
+        out = {}
+        for name, v in rows.items():
+            top = max(gs for gs, _ in v)
+            out[name] = (statistics.median(c for gs, c in v if gs == top), len(v))
+        return out
+
+    f, w = per_kernel(fetch_csv, "FETCH_SIZE"), per_kernel(write_csv, "WRITE_SIZE")
+    copies = [n for n in f if "copyBuffer" in n]
+    if not copies:
+        sys.exit("traffic summary: no copyBuffer dispatch in %s" % fetch_csv)
+    cf, cw = f[copies[0]][0], w[copies[0]][0]
+    kib = COPY_BYTES / 1024.0
+    sf, sw = kib / cf, kib / cw
+    out = {"_calibration": {"copy_bytes": COPY_BYTES, "copy_kernel": copies[0],
+                            "fetch_kib": cf, "write_kib": cw, "fetch_scale": round(sf, 4),
+                            "write_scale": round(sw, 4)}}
+    for name in sorted(f):
+        if not name.startswith("gemm_") or name not in w:
+            continue
+        out[name] = {"bytes": round((f[name][0] * sf + w[name][0] * sw) * 1024.0),
+                     "fetch_bytes": round(f[name][0] * sf * 1024.0),
+                     "write_bytes": round(w[name][0] * sw * 1024.0)}
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    with open(path, "w") as fh:
+        json.dump(out, fh, indent=1, sort_keys=True)
+    print("wrote %s: %d kernels, fetch scale %.4f, write scale %.4f" % (path, len(out) - 1, sf, sw))
 
 
 def bench_matvec(g, e, hb):

@@ -72,6 +72,10 @@ struct hb_gpu {
     double compile_seconds = 0.0;
     hb::Kernel zero_kernel;  // the fill kernel of hb_zero
     bool zero_built = false;
+    // The selection layer's cache flush (a SwiGLU pass over 384 MiB, more
+    // than the 256 MiB last-level cache), built on first use.
+    hb_buf flush_gu = 0, flush_h = 0;
+    int32_t flush_kernel = -1;
 };
 
 namespace hb {

@@ -321,6 +321,17 @@ int hb_download(hb_gpu* g, hb_buf buf, uint64_t offset, void* dst, uint64_t byte
     return HB_OK;
 }
 
+int hb_copy(hb_gpu* g, hb_range dst, hb_range src) {
+    char *pd, *ps;
+    uint64_t nd, ns;
+    int rc = resolve(g, dst, &pd, &nd);
+    if (rc || (rc = resolve(g, src, &ps, &ns))) return rc;
+    if (nd != ns) return fail(HB_ERR_INVALID, "hb_copy: ranges of different sizes");
+    if ((pd < ps + ns) && (ps < pd + nd) && nd) return fail(HB_ERR_INVALID, "hb_copy: ranges overlap");
+    HB_HIP(hipMemcpyAsync(pd, ps, nd, hipMemcpyDeviceToDevice, g->stream));
+    return HB_OK;
+}
+
 int hb_zero(hb_gpu* g, hb_buf buf, uint64_t offset, uint64_t bytes) {
     hb_range r{buf, 0, offset, bytes};
     char* p;
@@ -393,6 +404,11 @@ int hb_launch(hb_gpu* g, int32_t kernel, const hb_range* b, uint32_t nbind, uint
 }
 
 int hb_time(hb_gpu* g, const hb_op* ops, uint32_t nops, uint32_t reps, double* seconds) {
+    return hb_time_each(g, ops, nops, reps, seconds, nullptr);
+}
+
+int hb_time_each(hb_gpu* g, const hb_op* ops, uint32_t nops, uint32_t reps, double* seconds,
+                 double* op_seconds) {
     // Check every op once, then launch without re-checking.
     struct Ready {
         const Kernel* k;
@@ -421,18 +437,55 @@ int hb_time(hb_gpu* g, const hb_op* ops, uint32_t nops, uint32_t reps, double* s
         ready[i].m = op.m;
         ready[i].groups = groups_of(k.desc, op.m);
     }
-    HB_HIP(hipEventRecord(g->ev0, g->stream));
-    for (uint32_t r = 0; r < reps; r++)
-        for (auto& x : ready) {
-            int rc = launch_raw(g, *x.k, x.ptrs, x.n, x.m, x.groups);
-            if (rc) return rc;
+    if (!op_seconds) {
+        HB_HIP(hipEventRecord(g->ev0, g->stream));
+        for (uint32_t r = 0; r < reps; r++)
+            for (auto& x : ready) {
+                int rc = launch_raw(g, *x.k, x.ptrs, x.n, x.m, x.groups);
+                if (rc) return rc;
+            }
+        HB_HIP(hipEventRecord(g->ev1, g->stream));
+        HB_HIP(hipEventSynchronize(g->ev1));
+        float ms = 0;
+        HB_HIP(hipEventElapsedTime(&ms, g->ev0, g->ev1));
+        *seconds = ms * 1e-3;
+        return HB_OK;
+    }
+    // An event between consecutive launches (the same stream, so the
+    // launches still run back to back): event i..i+1 brackets launch i.
+    const size_t nev = (size_t)reps * nops + 1;
+    std::vector<hipEvent_t> ev(nev, nullptr);
+    int rc = HB_OK;
+    hipError_t he = hipSuccess;
+    for (auto& e : ev)
+        if ((he = hipEventCreate(&e)) != hipSuccess) {
+            rc = hip_fail(he, "hipEventCreate");
+            break;
         }
-    HB_HIP(hipEventRecord(g->ev1, g->stream));
-    HB_HIP(hipEventSynchronize(g->ev1));
-    float ms = 0;
-    HB_HIP(hipEventElapsedTime(&ms, g->ev0, g->ev1));
-    *seconds = ms * 1e-3;
-    return HB_OK;
+    size_t at = 0;
+    if (!rc && (he = hipEventRecord(ev[at++], g->stream)) != hipSuccess) rc = hip_fail(he, "hipEventRecord");
+    for (uint32_t r = 0; r < reps && !rc; r++)
+        for (auto& x : ready) {
+            if ((rc = launch_raw(g, *x.k, x.ptrs, x.n, x.m, x.groups))) break;
+            if ((he = hipEventRecord(ev[at++], g->stream)) != hipSuccess) {
+                rc = hip_fail(he, "hipEventRecord");
+                break;
+            }
+        }
+    if (!rc && (he = hipEventSynchronize(ev[nev - 1])) != hipSuccess) rc = hip_fail(he, "hipEventSynchronize");
+    if (!rc) {
+        for (uint32_t i = 0; i < nops; i++) op_seconds[i] = 0;
+        float ms = 0;
+        for (size_t j = 0; j + 1 < nev && !rc; j++) {
+            if ((he = hipEventElapsedTime(&ms, ev[j], ev[j + 1])) != hipSuccess) rc = hip_fail(he, "hipEventElapsedTime");
+            op_seconds[j % nops] += ms * 1e-3 / reps;
+        }
+        if (!rc && (he = hipEventElapsedTime(&ms, ev[0], ev[nev - 1])) != hipSuccess) rc = hip_fail(he, "hipEventElapsedTime");
+        *seconds = ms * 1e-3;
+    }
+    for (auto& e : ev)
+        if (e) hipEventDestroy(e);
+    return rc;
 }
 
 int hb_sync(hb_gpu* g) {

@@ -248,11 +248,18 @@ const Form kForms[10] = {
 };
 // Timed with the table but not named by gemm.mform: tiles whose counts
 // fill whole rounds of the 256 CUs on this build's shapes (256 x 192:
-// 768 tiles at 2048 x 18432; 128 x 160: 256 at 2048 x 2560), and the
-// band tile order of gemm_nax (prefill.rs:615-631).
+// 768 tiles at 2048 x 18432; 128 x 160: 256 at 2048 x 2560; 128 x 192:
+// 224 at 2048 x 2560, 8 wavefronts), three and four stages of 64 K for the
+// long-K shapes, and the band tile order of gemm_nax (prefill.rs:615-631).
 const Form kMoreForms[] = {
     {"mma_t256x192_w8", 256, 192, 64, 4, 2, 32, 1, 1, 1},
+    {"mma_t256x192_w8_x16", 256, 192, 64, 4, 2, 16, 1, 1, 1},
     {"mma_t128x160", 128, 160, 64, 2, 2, 16, 1, 1, 1},
+    {"mma_t128x160_s4", 128, 160, 64, 2, 2, 16, 3, 1, 0},
+    {"mma_t128x192_w8_s3", 128, 192, 64, 2, 4, 16, 2, 1, 0},
+    {"mma_t128x192_w8_s4", 128, 192, 64, 2, 4, 16, 3, 1, 0},
+    {"mma_t128x192_w8_s4_b2", 128, 192, 64, 2, 4, 16, 3, 1, 0, 2},
+    {"mma_t256x128_w8_s3", 256, 128, 64, 4, 2, 16, 2, 1, 1},
     {"mma_b2", 128, 128, 64, 2, 2, 16, 1, 1, 0, 2},
 };
 // The fused [gate | up] + SwiGLU forms (gate_up_pipes, qwen.rs:2148-2193):
@@ -367,23 +374,66 @@ struct hb_engine {
         return HB_OK;
     }
 
+    // The op that evicts the last-level cache: a SwiGLU pass reading 256 MiB
+    // and writing 128 MiB of the context's flush buffers.
+    int flush_op(hb_op* op) {
+        constexpr uint32_t F = 8192;
+        int rc;
+        if (g->flush_kernel < 0) {
+            hb_desc d{};
+            d.kind = HB_KIND_SWIGLU;
+            d.n = F;
+            int32_t k;
+            if ((rc = build(d, &k))) return rc;
+            if ((rc = hb_alloc(g, (uint64_t)F * 2 * F * 2, &g->flush_gu)) ||
+                (rc = hb_alloc(g, (uint64_t)F * F * 2, &g->flush_h)) ||
+                (rc = hb_zero(g, g->flush_gu, 0, (uint64_t)F * 2 * F * 2)))
+                return rc;
+            g->flush_kernel = k;
+        }
+        *op = make_op(g->flush_kernel, F, {hb_range{g->flush_gu, 0, 0, 0}, hb_range{g->flush_h, 0, 0, 0}});
+        return HB_OK;
+    }
+
+    // GPU seconds of `reps` runs of `ops`; cold: each run after the cache
+    // flush, only the ops' own launches counted (an event after each
+    // launch), so the weights come from HBM as in a layer step.
+    int run_ops(const std::vector<hb_op>& ops, uint32_t reps, bool cold, double* s) {
+        if (!cold) return time_ops(ops, reps, s);
+        std::vector<hb_op> seq(1);
+        int rc = flush_op(&seq[0]);
+        if (rc) return rc;
+        seq.insert(seq.end(), ops.begin(), ops.end());
+        std::vector<double> each(seq.size());
+        double total;
+        if ((rc = hb_time_each(g, seq.data(), (uint32_t)seq.size(), reps, &total, each.data()))) return rc;
+        *s = 0;
+        for (size_t i = 1; i < seq.size(); i++) *s += each[i] * reps;
+        return HB_OK;
+    }
+
     // pick_flagged (qwen.rs:2547-2575): reps so one run lasts ~2 ms, five
     // interleaved rounds, medians, the fastest eligible kept; logged with
-    // `*` after the ineligible.
+    // `*` after the ineligible.  cold (the dense GEMMs): every run after the
+    // cache flush -- MI355X's 256 MiB last-level cache would otherwise hold
+    // a candidate's W and X between its own runs, which a layer step never
+    // sees, and the ranking of warm runs is not the ranking in the step.
     int pick_flagged(const std::string& what, const std::vector<Cand>& c,
-                     const std::vector<bool>& eligible, size_t* best, double* best_s) {
+                     const std::vector<bool>& eligible, size_t* best, double* best_s,
+                     bool cold = false) {
         auto t0 = std::chrono::steady_clock::now();
         if (c.empty() || std::none_of(eligible.begin(), eligible.end(), [](bool e) { return e; }))
             return fail(HB_ERR_INVALID, what + ": no eligible candidate");
         int rc = heat(c[0].ops);
         double one;
-        if (rc || (rc = time_ops(c[0].ops, 1, &one)) || (rc = time_ops(c[0].ops, 1, &one))) return rc;
+        if (rc || (rc = run_ops(c[0].ops, 1, cold, &one)) || (rc = run_ops(c[0].ops, 1, cold, &one)))
+            return rc;
         uint32_t reps = (uint32_t)std::min(64.0, std::max(1.0, std::ceil(2e-3 / std::max(one, 1e-6))));
         std::vector<std::vector<double>> times(c.size());
         for (int round = 0; round < 5; round++)
             for (size_t i = 0; i < c.size(); i++) {
                 double s;
-                if ((rc = time_ops(c[i].ops, reps, &s))) return rc;
+                if ((rc = run_ops(c[i].ops, reps, cold, &s))) return rc;
                 times[i].push_back(s / reps);
             }
         std::vector<double> med(c.size());
@@ -608,7 +658,7 @@ int hb_engine_gemm(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, hb_range 
     uint32_t row_bytes = n * (out == HB_OUT_F32 ? 4 : 2);
     if ((rc = e->check_candidates(what, c, eligible, state, y, out == HB_OUT_F32, m, row_bytes))) return rc;
     size_t best;
-    if ((rc = e->pick_flagged(what, c, eligible, &best, nullptr))) return rc;
+    if ((rc = e->pick_flagged(what, c, eligible, &best, nullptr, true))) return rc;
     e->gemm_pick[key] = c[best].kernel;
     *kernel = c[best].kernel;
     return HB_OK;
@@ -666,7 +716,7 @@ int hb_engine_gate_up(hb_engine* e, uint32_t h, uint32_t inter, hb_range state, 
     if (fswi == 1) return c[0].name == "apart" ? keep(gk, sk) : keep(c[0].kernel, -1);
     if ((rc = e->check_candidates(what, c, eligible, state, hout, false, m, inter * 2))) return rc;
     size_t best;
-    if ((rc = e->pick_flagged(what, c, eligible, &best, nullptr))) return rc;
+    if ((rc = e->pick_flagged(what, c, eligible, &best, nullptr, true))) return rc;
     return best == 0 ? keep(gk, sk) : keep(c[best].kernel, -1);
 }
 

@@ -141,14 +141,16 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     const u32* __restrict__ state, const u16* __restrict__ W, const u16* __restrict__ X,
     void* __restrict__ Yv, const u32* __restrict__ list, const u32* __restrict__ tiles,
     u32 m_launch) {
-    // The stages as distinct LDS objects, so that the compiler sees that one
-    // stage's direct-to-LDS loads never alias another stage's reads.
+#if HB_DMA
+    // The stages, one after another in one LDS array per operand; the stage
+    // in use is a scalar index, so any count of K tiles runs one loop body.
+    __shared__ u32x4 sXa[NS * XCHP], sWa[NS * WCHP];
+#else
+    // Register staging: the stages as distinct LDS objects, so that the
+    // compiler sees that one stage's stores never alias the other's reads.
     __shared__ u32x4 sX0[XCHP], sW0[WCHP];
     __shared__ u32x4 sX1[NS > 1 ? XCHP : 1], sW1[NS > 1 ? WCHP : 1];
-    __shared__ u32x4 sX2[NS > 2 ? XCHP : 1], sW2[NS > 2 ? WCHP : 1];
-    __shared__ u32x4 sX3[NS > 3 ? XCHP : 1], sW3[NS > 3 ? WCHP : 1];
-#define STX(i) ((i) == 0 ? sX0 : (i) == 1 ? sX1 : (i) == 2 ? sX2 : sX3)
-#define STW(i) ((i) == 0 ? sW0 : (i) == 1 ? sW1 : (i) == 2 ? sW2 : sW3)
+#endif
 
     const u32 tid = threadIdx.x, lane = tid & 63u;
     const u32 wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar
@@ -328,60 +330,72 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
                             "s"(kb) : "memory");
     };
     constexpr u32 LDT = X_LD + W_LD;  // load instructions per tile per lane
+    auto stx = [&](u32 i) HB_INLINE -> u32x4* { return sXa + i * XCHP; };
+    auto stw = [&](u32 i) HB_INLINE -> u32x4* { return sWa + i * WCHP; };
     // Prologue: tiles 0..NS-2 in flight, tile 0 landed and published.
 #pragma unroll
     for (u32 t = 0; t + 1 < NS; t++)
-        if (t < KT) load_stage(t, STX(t), STW(t));
-    if (NS == 1) load_stage(0, sX0, sW0);
+        if (t < KT) load_stage(t, stx(t), stw(t));
+    if (NS == 1) load_stage(0, stx(0), stw(0));
     if (NS > 2 && KT > NS - 2) WAIT_VM((NS - 2) * LDT);
     else WAIT_VM(0);
     STAGE_BARRIER();
-    read_frags(sX0, sW0, 0, 0);
+    read_frags(stx(0), stw(0), 0, 0);
 
-    // KT is a multiple of NS (NS > 1), so every unrolled tile runs the same
-    // code: one MFMA site per step keeps the accumulators in AGPRs.  Past
-    // the last tile the "next" fragments are read from a stale stage and
-    // never used.
-    static_assert(NS == 1 || KT % NS == 0, "K tiles a multiple of the stages");
-    for (u32 kt0 = 0; kt0 < KT; kt0 += NS) {
+    // The stage step of K tile kt, whose stage is `cur` (next: `nxt`, the
+    // one to load: `ld`).  Past the last tile the "next" fragments are read
+    // from a stale stage and never used.
+    auto tile_step = [&](u32 kt, u32 cur, u32 nxt, u32 ld) HB_INLINE {
+        if constexpr (NS > 1) {
+            // Tile kt + NS - 1 into the stage tile kt - 1 used; every wave
+            // passed the barrier after its last read of it.
+            const bool more = kt + NS - 1 < KT;
+            if (more) load_stage(kt + NS - 1, stx(ld), stw(ld));
+            steps(stx(cur), stw(cur));
+            // Tile kt + 1 landed (its loads are the oldest in flight),
+            // published, and its first fragments read under the last MFMAs
+            // of tile kt.
+            if (more) WAIT_VM((NS - 2) * LDT);
+            else WAIT_VM(0);
+            STAGE_BARRIER();
+            read_frags(stx(nxt), stw(nxt), 0, S & 1);
+            mfmas((S - 1) & 1);
+            interleave();
+            __builtin_amdgcn_sched_barrier(0);
+        } else {
+            steps(stx(0), stw(0));
+            // One stage: every wave done with it, then the next tile.
+            STAGE_BARRIER();
+            if (kt + 1 < KT) load_stage(kt + 1, stx(0), stw(0));
+            WAIT_VM(0);
+            STAGE_BARRIER();
+            read_frags(stx(0), stw(0), 0, S & 1);
+            mfmas((S - 1) & 1);
+        }
+        // The next tile's step 0 is in a[S & 1]; steps() expects a[0].
+        if constexpr (S & 1) {
 #pragma unroll
-        for (u32 bi = 0; bi < NS; bi++) {
-            const u32 kt = kt0 + bi;
-            u32x4* cx = STX(bi);
-            u32x4* cw = STW(bi);
-            if constexpr (NS > 1) {
-                // Tile kt + NS - 1 into the stage tile kt - 1 used; every wave
-                // passed the barrier after its last read of it.
-                if (kt + NS - 1 < KT)
-                    load_stage(kt + NS - 1, STX((bi + NS - 1) % NS), STW((bi + NS - 1) % NS));
-                steps(cx, cw);
-                // Tile kt + 1 landed (its loads are the oldest in flight),
-                // published, and its first fragments read under the last
-                // MFMAs of tile kt.
-                if (kt + NS - 1 < KT) WAIT_VM((NS - 2) * LDT);
-                else WAIT_VM(0);
-                STAGE_BARRIER();
-                read_frags(STX((bi + 1) % NS), STW((bi + 1) % NS), 0, S & 1);
-                mfmas((S - 1) & 1);
-                interleave();
-                __builtin_amdgcn_sched_barrier(0);
-            } else {
-                steps(cx, cw);
-                // One stage: every wave done with it, then the next tile.
-                STAGE_BARRIER();
-                if (kt + 1 < KT) load_stage(kt + 1, sX0, sW0);
-                WAIT_VM(0);
-                STAGE_BARRIER();
-                read_frags(sX0, sW0, 0, S & 1);
-                mfmas((S - 1) & 1);
-            }
-            // The next tile's step 0 is in a[S & 1]; steps() expects a[0].
-            if constexpr (S & 1) {
+            for (u32 i = 0; i < IN; i++) a[0][i] = a[1][i];
 #pragma unroll
-                for (u32 i = 0; i < IN; i++) a[0][i] = a[1][i];
+            for (u32 j = 0; j < IM; j++) b[0][j] = b[1][j];
+        }
+    };
+    // One MFMA site per step keeps the accumulators in registers: a K tile
+    // count that is a multiple of the stages runs the loop unrolled by NS
+    // (every stage at a constant LDS offset), any other one loop body with
+    // the stage as a scalar index.
+    if constexpr (KT % NS == 0) {
+        for (u32 kt0 = 0; kt0 < KT; kt0 += NS) {
 #pragma unroll
-                for (u32 j = 0; j < IM; j++) b[0][j] = b[1][j];
-            }
+            for (u32 bi = 0; bi < NS; bi++)
+                tile_step(kt0 + bi, bi, (bi + 1) % NS, (bi + NS - 1) % NS);
+        }
+    } else {
+        u32 cur = 0;
+        for (u32 kt = 0; kt < KT; kt++) {
+            const u32 nxt = cur + 1 == NS ? 0 : cur + 1;
+            tile_step(kt, cur, nxt, cur == 0 ? NS - 1 : cur - 1);
+            cur = nxt;
         }
     }
 #else

@@ -149,6 +149,7 @@ lib.hb_free.argtypes = [_P, _u32]
 lib.hb_upload.argtypes = [_P, _u32, _u64, _P, _u64]
 lib.hb_download.argtypes = [_P, _u32, _u64, _P, _u64]
 lib.hb_zero.argtypes = [_P, _u32, _u64, _u64]
+lib.hb_copy.argtypes = [_P, Range, Range]
 lib.hb_buffer_ptr.argtypes = [_P, _u32, ctypes.POINTER(_P)]
 lib.hb_kernel_build.argtypes = [_P, ctypes.POINTER(Desc), ctypes.POINTER(_i32)]
 lib.hb_kernel_name.argtypes = [_P, _i32]
@@ -161,6 +162,8 @@ lib.hb_compile_seconds.argtypes = [_P]
 lib.hb_compile_seconds.restype = ctypes.c_double
 lib.hb_launch.argtypes = [_P, _i32, ctypes.POINTER(Range), _u32, _u32]
 lib.hb_time.argtypes = [_P, ctypes.POINTER(Op), _u32, _u32, ctypes.POINTER(ctypes.c_double)]
+lib.hb_time_each.argtypes = [_P, ctypes.POINTER(Op), _u32, _u32, ctypes.POINTER(ctypes.c_double),
+                             ctypes.POINTER(ctypes.c_double)]
 lib.hb_sync.argtypes = [_P]
 lib.hb_fill_normal_bf16.argtypes = [_u64, ctypes.c_float, _P, _u64, ctypes.c_int]
 lib.hb_fill_normal_bf16.restype = None
@@ -318,6 +321,10 @@ class Gpu:
         n = self._sizes[int(buf)] - offset if nbytes is None else nbytes
         check(lib.hb_zero(self.h, int(buf), int(offset), int(n)))
 
+    def copy(self, dst, src):
+        """Device-to-device copy of Range src into Range dst (same size)."""
+        check(lib.hb_copy(self.h, dst, src))
+
     def size(self, buf):
         return self._sizes[int(buf)]
 
@@ -348,6 +355,15 @@ class Gpu:
         s = ctypes.c_double()
         check(lib.hb_time(self.h, arr, len(ops), int(reps), ctypes.byref(s)))
         return s.value
+
+    def time_each(self, ops, reps=1):
+        """(GPU seconds of `reps` runs of `ops`, mean seconds of each op), one
+        event after every launch on the library's stream."""
+        arr = (Op * len(ops))(*ops)
+        s = ctypes.c_double()
+        each = (ctypes.c_double * len(ops))()
+        check(lib.hb_time_each(self.h, arr, len(ops), int(reps), ctypes.byref(s), each))
+        return s.value, list(each)
 
     def sync(self):
         check(lib.hb_sync(self.h))

@@ -59,6 +59,11 @@ int hb_upload(hb_gpu *gpu, hb_buf buf, uint64_t offset, const void *src, uint64_
 int hb_download(hb_gpu *gpu, hb_buf buf, uint64_t offset, void *dst, uint64_t bytes);
 /* Zero `bytes` at `offset` with a fill kernel on the context's stream. */
 int hb_zero(hb_gpu *gpu, hb_buf buf, uint64_t offset, uint64_t bytes);
+/* Device-to-device copy of `src` into `dst` (equal sizes, no overlap) on the
+ * context's stream, by HIP's copy kernel.  No counterpart in the reference,
+ * whose buffers are shared with the CPU; for callers that stage device
+ * buffers, and the plain copy that calibrates the traffic counters. */
+int hb_copy(hb_gpu *gpu, hb_range dst, hb_range src);
 /* Device address of a buffer (for callers that bring their own kernels). */
 int hb_buffer_ptr(hb_gpu *gpu, hb_buf buf, void **ptr);
 
@@ -165,6 +170,12 @@ typedef struct hb_op { /* Op {pipe, ranges, groups} (qwen.rs:650-655) */
 /* time_ops (qwen.rs:2593): `reps` runs of `ops` in order on the stream,
  * timed by two HIP events on that stream; *seconds = the GPU time of all. */
 int hb_time(hb_gpu *gpu, const hb_op *ops, uint32_t nops, uint32_t reps, double *seconds);
+/* hb_time with an event recorded after every launch on the same stream:
+ * op_seconds[i] = the mean duration of op i over the reps (the
+ * time_ops-per-pipe breakdown of the reference's --profile, qwen.rs:2593),
+ * *seconds the whole run. */
+int hb_time_each(hb_gpu *gpu, const hb_op *ops, uint32_t nops, uint32_t reps, double *seconds,
+                 double *op_seconds);
 /* submit_wait (metal/gpu.rs:209-221): wait for the stream. */
 int hb_sync(hb_gpu *gpu);
 

@@ -21,6 +21,9 @@ TILES = {
     "t128x128_reg_d1": dict(bm=128, bn=128, bk=64, wm=2, wn=2, mfma=16, dbuf=1, lds_dma=0, order=0),
     "t64x64_reg_s1": dict(bm=64, bn=64, bk=32, wm=1, wn=4, mfma=16, dbuf=0, lds_dma=0, order=0),
     "t256x192_w8_x32": dict(bm=256, bn=192, bk=64, wm=4, wn=2, mfma=32, dbuf=1, lds_dma=1, order=1),
+    "t128x192_w8_s3": dict(bm=128, bn=192, bk=64, wm=2, wn=4, mfma=16, dbuf=2, lds_dma=1, order=0),
+    "t128x192_w8_s4": dict(bm=128, bn=192, bk=64, wm=2, wn=4, mfma=16, dbuf=3, lds_dma=1, order=0),
+    "t128x160_s3_k32": dict(bm=128, bn=160, bk=32, wm=2, wn=2, mfma=16, dbuf=2, lds_dma=1, order=1),
     "t128x160_x16": dict(bm=128, bn=160, bk=64, wm=2, wn=2, mfma=16, dbuf=1, lds_dma=1, order=1),
     "t128x128_band2": dict(bm=128, bn=128, bk=64, wm=2, wn=2, mfma=16, dbuf=1, lds_dma=1, order=0,
                            band=2),
@@ -180,3 +183,24 @@ def test_gemm_bindings_checked(gpu):
     assert "X" in str(e.value)
     for b in (st, W, X, Y):
         gpu.free(b)
+
+
+def test_time_each_brackets_every_launch(gpu):
+    """hb_time_each: the per-op means telescope to the whole run's time, and
+    the larger GEMM takes longer than the smaller one."""
+    k, m = 2048, 2048
+    x = hb.normal_bf16(1, 1.0, (m, k))
+    ws = [hb.normal_bf16(2, 0.02, (n, k)) for n in (512, 16384)]
+    st = gpu.alloc_with(np.array([0, 0, 0, m], np.uint32))
+    X = gpu.alloc_with(x)
+    bufs, ops = [st, X], []
+    for w in ws:
+        W, Y = gpu.alloc_with(w), gpu.alloc(m * w.shape[0] * 2)
+        bufs += [W, Y]
+        kern = gpu.pipeline(hb.gemm_mma(k, w.shape[0], 0))
+        ops.append(hb.Op(kern, [hb.r(st), hb.r(W), hb.r(X), hb.r(Y), hb.r(st), hb.r(st)], m))
+    total, each = gpu.time_each(ops, 7)
+    for b in bufs:
+        gpu.free(b)
+    assert abs(sum(each) * 7 - total) <= 1e-3 * total + 1e-6
+    assert each[1] > 4 * each[0] > 0
