@@ -239,6 +239,12 @@ int emit(const hb_desc& d, Emitted* e) {
             e->nbind = 3;
             e->defines = {D("HB_OP", 6), D("HB_E", 64), D("HB_TOPK", d.top_k), D("HB_D", d.n)};
             return HB_OK;
+        case HB_KIND_ROUND_PROBE:
+            e->name = "round_probe_bf16";
+            e->source = "probe.hip";
+            e->threads = 256;
+            e->nbind = 3;
+            return HB_OK;
         default:
             return fail(HB_ERR_UNSUPPORTED, "kernel kind " + std::to_string(d.kind) + " not built");
     }
@@ -271,6 +277,8 @@ uint32_t groups_of(const hb_desc& d, uint32_t m) {
         case HB_KIND_SWIGLU:
         case HB_KIND_COMBINE:
             return (uint32_t)(((uint64_t)m * (d.n / 8) + 255) / 256);
+        case HB_KIND_ROUND_PROBE:
+            return (1u << 24) / 256;  // one pattern per thread
         default:
             return 0;
     }
@@ -333,6 +341,10 @@ int check_bindings(const hb_desc& d, const uint64_t* s, uint32_t nbind, uint32_t
         case HB_KIND_SWIGLU:
             if ((rc = need(s, 0, mm * 2 * d.n * 2, "gate_up"))) return rc;
             return need(s, 1, mm * d.n * 2, "h");
+        case HB_KIND_ROUND_PROBE:
+            if ((rc = need(s, 0, 16, "state"))) return rc;
+            if ((rc = need(s, 1, 2ull << 24, "out_int"))) return rc;
+            return need(s, 2, 2ull << 24, "out_hw");
         case HB_KIND_COMBINE:
             if ((rc = need(s, 0, mm * d.top_k * d.n * 2, "y"))) return rc;
             if ((rc = need(s, 1, mm * k2 * 4, "route"))) return rc;

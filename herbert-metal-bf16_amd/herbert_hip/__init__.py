@@ -73,6 +73,7 @@ class Kind(enum.IntEnum):
     GATHER = 8
     SWIGLU = 9
     COMBINE = 10
+    ROUND_PROBE = 11
 
 
 class Rows(enum.IntEnum):

@@ -80,7 +80,8 @@ enum hb_kind {
     HB_KIND_SORT_ATOMIC = 7, /* moe_sort_atomic (prefill.rs:1450-1531) */
     HB_KIND_GATHER = 8,      /* moe_gather (prefill.rs:579-610) */
     HB_KIND_SWIGLU = 9,      /* swiglu_slots / swiglu_rows (qwen_kernels.rs:2087-2117) */
-    HB_KIND_COMBINE = 10     /* moe_combine (qwen_kernels.rs:2119-2165) */
+    HB_KIND_COMBINE = 10,    /* moe_combine (qwen_kernels.rs:2119-2165) */
+    HB_KIND_ROUND_PROBE = 11 /* herbert-metal-probe round (bin/herbert-metal-probe.rs:7-11) */
 };
 
 enum hb_out { /* Out (kernels.rs:30-43) */
@@ -155,7 +156,7 @@ double hb_compile_seconds(hb_gpu *gpu);
  *   MATVEC: W, x, y          ROUTE: scores, route
  *   SORT, SORT_ATOMIC: state, route, list, tiles
  *   GATHER: state, list, X, XS        SWIGLU: gate_up, h
- *   COMBINE: y, route, out
+ *   COMBINE: y, route, out    ROUND_PROBE: state (state[0] = chunk), out_int, out_hw
  * `m` is the rows of the block (the kernels read state[3], never beyond m). */
 int hb_launch(hb_gpu *gpu, int32_t kernel, const hb_range *bindings, uint32_t nbind, uint32_t m);
 

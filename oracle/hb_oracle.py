@@ -67,6 +67,13 @@ def threads_default():
     return min(16, os.cpu_count() or 1)
 
 
+def rne_range(first, n):
+    """hbo_f32_to_bf16_range: the bf16 RNE of the f32 patterns first..first+n-1."""
+    out = np.empty(n, np.uint16)
+    lib.hbo_f32_to_bf16_range(first, n, _p(out))
+    return out
+
+
 def gemm(x, w, out=OUT_BF16, y=None, threads=None):
     """Y[m][n] = X[m][k] . W[n][k]^T under the contract; y: Residual's input."""
     x = _c(x, np.uint16)
