@@ -788,7 +788,10 @@ int hb_engine_matvec(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, uint32_
     if (c.empty()) return fail(HB_ERR_COMPILE, std::string("matvec ") + key + ": no form built");
     std::vector<bool> all(c.size(), true);
     size_t best;
-    int rc = e->pick_flagged(std::string("matvec ") + key, c, all, &best, nullptr);
+    // Cold as in a decode step (a model's weights are far larger than the
+    // 256 MiB last-level cache, every matrix is read from HBM once per
+    // token): the flush before each run, only the matvec launches counted.
+    int rc = e->pick_flagged(std::string("matvec ") + key, c, all, &best, nullptr, true);
     if (rc) return rc;
     e->mv_pick[key] = descs[best];
     *kernel = c[best].kernel;

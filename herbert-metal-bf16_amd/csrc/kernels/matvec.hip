@@ -58,6 +58,10 @@ HB_DEV void store_out(void* y, u64 at, float v) {
     }
 }
 
+struct HbTrue { static constexpr bool value = true; };
+struct HbFalse { static constexpr bool value = false; };
+#define HB_INLINE2 __attribute__((always_inline))
+
 HB_DEV float wave_sum(float v) {
     // Butterfly over the 64 lanes (xor 32, 16, ..., 1).
 #pragma unroll
@@ -93,21 +97,32 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
             u32 n = n0 + r;
             wr[r] = W + (u64)(n < N ? n : N - 1) * K;
         }
-        constexpr u32 CHUNKS = KS / 8;
-        u32 c = lane;
-        for (; c + 64 * (U - 1) < CHUNKS; c += 64 * U) {
+        // Blocks of 64*U chunks: lane l takes chunks l, l+64, ..., all U
+        // loads of every row issued before the first fma; the last block
+        // (K not a multiple of the block) predicated per chunk, its loads
+        // still issued together.
+        constexpr u32 CHUNKS = KS / 8, BLK = 64 * U;
+        constexpr u32 NFULL = CHUNKS / BLK, REM = CHUNKS % BLK;
+        auto block = [&](u32 c0, auto full) HB_INLINE2 {
             u32x4 wv[U][RB];
 #pragma unroll
-            for (u32 u = 0; u < U; u++)
+            for (u32 u = 0; u < U; u++) {
+                if (!decltype(full)::value && u * 64 >= REM) break;  // no lane has this chunk
+                const bool on = decltype(full)::value || (u * 64 + 64 <= REM) || (c0 + 64 * u < CHUNKS);
 #pragma unroll
                 for (u32 r = 0; r < RB; r++)
-                    wv[u][r] = __builtin_nontemporal_load((const u32x4*)(wr[r] + k0 + (c + 64 * u) * 8));
+                    wv[u][r] = on ? __builtin_nontemporal_load((const u32x4*)(wr[r] + k0 + (c0 + 64 * u) * 8))
+                                  : u32x4{0u, 0u, 0u, 0u};
+            }
 #pragma unroll
             for (u32 u = 0; u < U; u++) {
+                if (!decltype(full)::value && u * 64 >= REM) break;  // no lane has this chunk
+                const bool on = decltype(full)::value || (u * 64 + 64 <= REM) || (c0 + 64 * u < CHUNKS);
 #pragma unroll
                 for (u32 j = 0; j < MV; j++) {
                     if (j >= m) break;
-                    const u32x4 xv = *(const u32x4*)(x + (u64)j * K + k0 + (c + 64 * u) * 8);
+                    const u32x4 xv = on ? *(const u32x4*)(x + (u64)j * K + k0 + (c0 + 64 * u) * 8)
+                                        : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
                     for (u32 r = 0; r < RB; r++) {
                         float a = acc[r][j];
@@ -120,25 +135,9 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
                     }
                 }
             }
-        }
-        for (; c < CHUNKS; c += 64) {
-#pragma unroll
-            for (u32 j = 0; j < MV; j++) {
-                if (j >= m) break;
-                const u32x4 xv = *(const u32x4*)(x + (u64)j * K + k0 + c * 8);
-#pragma unroll
-                for (u32 r = 0; r < RB; r++) {
-                    const u32x4 wv = *(const u32x4*)(wr[r] + k0 + c * 8);
-                    float a = acc[r][j];
-#pragma unroll
-                    for (u32 e = 0; e < 4; e++) {
-                        a = __builtin_fmaf(bf16_lo(wv[e]), bf16_lo(xv[e]), a);
-                        a = __builtin_fmaf(bf16_hi(wv[e]), bf16_hi(xv[e]), a);
-                    }
-                    acc[r][j] = a;
-                }
-            }
-        }
+        };
+        for (u32 bi = 0; bi < NFULL; bi++) block(bi * BLK + lane, HbTrue{});
+        if constexpr (REM != 0) block(NFULL * BLK + lane, HbFalse{});
 #pragma unroll
         for (u32 r = 0; r < RB; r++)
 #pragma unroll
