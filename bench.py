@@ -10,7 +10,8 @@ picked at load (QwenEngine::gemm with gemm.auto, src/metal/qwen.rs:2200).
 `value` = the step's algorithmic flops (2*M*N*K summed) / its GPU time,
 inputs resident in HBM, timed with HIP events on the library's stream.
 
-Also reported (the metric's second half): the decode matvec, M=1, over
+Also reported: BASELINE config 5's MoE layer (the grouped expert GEMMs
+against HBM, and as TFLOP/s), and (the metric's second half) the decode matvec, M=1, over
 four layers of the same weights plus the lm_head (K=2560, N=151936), 2.2 GB
 streamed per step, as GB/s of algorithmic bytes (2*N*K + 2*M*K + 2*M*N per
 projection, + 2*M*N for Residual) against HBM's 8 TB/s.
@@ -86,6 +87,7 @@ def main():
     ap.add_argument("--cpu-rows", type=int, default=1536)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-matvec", action="store_true")
+    ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--traffic-run", action="store_true")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     args = ap.parse_args()
@@ -164,6 +166,8 @@ def main():
 
     if not args.no_matvec:
         result["matvec"] = bench_matvec(g, e, hb)
+    if not args.no_moe:
+        result["moe"] = bench_moe(g, e, hb)
     e.log_summary()
     e.close()
     g.close()
@@ -228,6 +232,51 @@ def traffic_summary(fetch_csv, write_csv):
     with open(path, "w") as fh:
         json.dump(out, fh, indent=1, sort_keys=True)
     print("wrote %s: %d kernels, fetch scale %.4f, write scale %.4f" % (path, len(out) - 1, sf, sw))
+
+
+def bench_moe(g, e, hb):
+    """one MoE layer's routed experts over T=2048 tokens,
+    256 experts, top 8 (16384 pairs), hidden 2048, expert intermediate 512,
+    on the kernels expert_pipes picked: route -> sort -> [gather] -> grouped
+    gate|up -> SwiGLU -> grouped down -> combine.  The grouped GEMMs are
+    HBM-bound (1.07 GB + 0.54 GB of expert weights); their algorithmic bytes
+    are 2*(experts with rows)*N*K + 2*P*K + 2*P*N, flops 2*P*N*K."""
+    T, E, TOPK, H, MI = 2048, 256, 8, 2048, 512
+    seed = 0x5EED0005
+    wgu = g.alloc_with(hb.normal_bf16(seed + 1, 0.02, (E * 2 * MI, H)))
+    wdn = g.alloc_with(hb.normal_bf16(seed + 2, 0.02, (E * H, MI)))
+    layer = hb.MoeLayer(g, e, E, TOPK, H, MI, T, wgu, wdn, scores=hb.normal_bf16(seed, 1.0, (T, E)),
+                        x=hb.normal_bf16(seed + 3, 1.0, (T, H)))
+    ops = layer.ops()
+    g.time_ops(ops, 3)
+    reps = 20
+    t, each = g.time_each(ops, reps)
+    route = g.download(layer.buf["route"], np.uint32, T * 2 * TOPK).reshape(T, 2 * TOPK)
+    used = len(np.unique(route[:, :TOPK]))
+    P = T * TOPK
+    names = ["route", "sort"] + (["gather"] if layer.kernels[3] >= 0 else []) + \
+        ["gate_up", "swiglu", "down", "combine"]
+    per = dict(zip(names, each))
+    gu_b = 2.0 * used * 2 * MI * H + 2.0 * P * H + 2.0 * P * 2 * MI
+    dn_b = 2.0 * used * H * MI + 2.0 * P * MI + 2.0 * P * H
+    gu_f, dn_f = 2.0 * P * 2 * MI * H, 2.0 * P * H * MI
+    out = {"unit": "GB/s", "peak": HBM_PEAK, "layer_us": round(t / reps * 1e6, 2),
+           "experts_with_rows": used, "rows_per_tile": layer.bm,
+           "gate_up": {"us": round(per["gate_up"] * 1e6, 2), "gbs": round(gu_b / per["gate_up"] / 1e9, 1),
+                       "frac": round(gu_b / per["gate_up"] / 1e9 / HBM_PEAK, 4),
+                       "tflops": round(gu_f / per["gate_up"] / 1e12, 1),
+                       "kernel": g.kernel_name(layer.kernels[1])},
+           "down": {"us": round(per["down"] * 1e6, 2), "gbs": round(dn_b / per["down"] / 1e9, 1),
+                    "frac": round(dn_b / per["down"] / 1e9 / HBM_PEAK, 4),
+                    "tflops": round(dn_f / per["down"] / 1e12, 1),
+                    "kernel": g.kernel_name(layer.kernels[2])},
+           "ops_us": {nm: round(v * 1e6, 2) for nm, v in per.items()}}
+    out["value"] = round((gu_b + dn_b) / (per["gate_up"] + per["down"]) / 1e9, 1)
+    out["frac"] = round(out["value"] / HBM_PEAK, 4)
+    layer.free()
+    g.free(wgu)
+    g.free(wdn)
+    return out
 
 
 def bench_matvec(g, e, hb):

@@ -813,8 +813,10 @@ int hb_engine_experts(hb_engine* e, uint32_t experts, uint32_t top_k, uint32_t h
         d.rows_max = m;
         return d;
     };
-    // An expert GEMM over tiles of bm rows: W rows by bn, four waves along N.
-    auto gemm_desc = [&](uint32_t k, uint32_t n, uint32_t rows_of, uint32_t bm, uint32_t bn) {
+    // An expert GEMM over tiles of bm rows: W rows by bn, wm x wn waves
+    // (default four along N), stages - 1 = dbuf.
+    auto gemm_desc = [&](uint32_t k, uint32_t n, uint32_t rows_of, uint32_t bm, uint32_t bn,
+                         uint32_t wm = 1, uint32_t wn = 4, uint32_t dbuf = 1) {
         hb_desc d{};
         d.kind = HB_KIND_GEMM;
         d.k = k;
@@ -825,11 +827,11 @@ int hb_engine_experts(hb_engine* e, uint32_t experts, uint32_t top_k, uint32_t h
         d.bm = bm;
         d.bn = bn;
         d.bk = 64;
-        d.wm = 1;
-        d.wn = 4;
+        d.wm = wm;
+        d.wn = wn;
         d.mfma = 16;
-        d.lds_dma = (bm * 8) % 256 == 0 && (k / 64) % 2 == 0 ? 1 : 0;
-        d.dbuf = 1;
+        d.lds_dma = 1;
+        d.dbuf = dbuf;
         d.top_k = top_k;
         d.experts = experts;
         d.tiles = (m * top_k + bm - 1) / bm + experts;  // moe_tiles
@@ -860,8 +862,11 @@ int hb_engine_experts(hb_engine* e, uint32_t experts, uint32_t top_k, uint32_t h
     };
     hb_op dn_op = make_op(0, m, {io->state, io->w_down, io->ehb, io->ey, io->list, io->tiles});
     hb_op g_op = make_op(gather, m, {io->state, io->list, io->x, io->xs});
+    // moe.tile's 16, 32, 64, and (timed only) 128: at ~64 rows per expert a
+    // tile of 128 holds every row of most experts, so each expert's W is
+    // read once (HBM-bound) at the price of MFMA work on padding rows.
     std::vector<uint32_t> tiles_rows = t.moe_tile_set ? std::vector<uint32_t>{t["moe.tile"]}
-                                                      : std::vector<uint32_t>{16, 32, 64};
+                                                      : std::vector<uint32_t>{16, 32, 64, 128};
     double best_total = 1e30;
     for (uint32_t bm : tiles_rows) {
         int32_t scan, atomic, mma_gu, mma_dn;
@@ -904,8 +909,10 @@ int hb_engine_experts(hb_engine* e, uint32_t experts, uint32_t top_k, uint32_t h
         add_gu("mma", gemm_desc(hidden, 2 * inter, HB_ROWS_GATHER, bm, 128), false);
         add_gu("mma_n256", gemm_desc(hidden, 2 * inter, HB_ROWS_GATHER, bm, 256), false);
         add_gu("gather+mma", gemm_desc(hidden, 2 * inter, HB_ROWS_SORTED, bm, 128), true);
+        if (bm >= 32) add_gu("mma_w2x2", gemm_desc(hidden, 2 * inter, HB_ROWS_GATHER, bm, 128, 2, 2), false);
         add_dn("mma", gemm_desc(inter, hidden, HB_ROWS_SCATTER, bm, 128));
         add_dn("mma_n256", gemm_desc(inter, hidden, HB_ROWS_SCATTER, bm, 256));
+        if (bm >= 32) add_dn("mma_w2x4_s3", gemm_desc(inter, hidden, HB_ROWS_SCATTER, bm, 128, 2, 4, 2));
         size_t bgu, bdn;
         double s_gu, s_dn;
         snprintf(what, sizeof what, "experts gate_up %ux%u by %u rows, %u rows", hidden, 2 * inter, bm, m);

@@ -466,9 +466,12 @@ class MoeLayer:
     in the reference's op order (qwen.rs:2705-2735): route_qwen -> moe_sort
     -> [moe_gather] -> grouped gate|up -> swiglu_slots -> grouped down
     (scatter to slot rows) -> moe_combine.  Owns its device buffers; the
-    kernels come from Engine.experts (expert_pipes)."""
+    kernels come from Engine.experts (expert_pipes), timed on the route of
+    `scores` ([rows][experts] bf16, routed here first: the reference's
+    real_route, qwen.rs:2340) and `x` if given."""
 
-    def __init__(self, gpu, engine, experts, top_k, hidden, inter, rows, w_gate_up, w_down):
+    def __init__(self, gpu, engine, experts, top_k, hidden, inter, rows, w_gate_up, w_down,
+                 scores=None, x=None):
         self.gpu, self.e, self.k, self.h, self.mi, self.rows = gpu, experts, top_k, hidden, inter, rows
         pairs = rows * top_k
         g = gpu
@@ -493,6 +496,12 @@ class MoeLayer:
         self.route_k = gpu.pipeline(Desc(kind=Kind.ROUTE, experts=experts, top_k=top_k))
         self.swiglu_k = gpu.pipeline(Desc(kind=Kind.SWIGLU, n=inter))
         self.combine_k = gpu.pipeline(Desc(kind=Kind.COMBINE, n=hidden, top_k=top_k))
+        if x is not None:
+            g.upload(b["x"], x)
+        if scores is not None:
+            g.upload(b["scores"], scores)
+            g.launch(self.route_k, [r(b["scores"]), r(b["route"])], rows)
+            g.sync()
         self.kernels, self.bm = engine.experts(experts, top_k, hidden, inter, rows, self.io)
 
     def ops(self, m=None):

@@ -232,8 +232,11 @@ int hb_engine_matvec(hb_engine *engine, uint32_t k, uint32_t n, uint32_t out, ui
 /* QwenEngine::expert_pipes (qwen.rs:2326-2391): the sort, the grouped
  * gate_up GEMM (Gather) and down GEMM (Scatter) of an MoE layer of `experts`
  * experts, top_k slots, hidden `hidden`, expert intermediate `inter`, for
- * blocks of m rows: with gemm.auto, tiles of 16, 32 and 64 rows (moe.tile
- * only, if given) each timed, the tile whose kernels sum the least kept.
+ * blocks of m rows: with gemm.auto, tiles of 16, 32, 64 and 128 rows
+ * (moe.tile only, if given) each timed, the tile whose kernels sum the least
+ * kept.  The route buffer must hold a real route of m rows when this runs
+ * (the reference times these only after a first prefill, real_route,
+ * qwen.rs:2340): the tiles and the expert weights read follow from it.
  * Buffers: state, route [m][2*top_k], list, tiles, X [m][hidden], the
  * experts' gate_up W [experts*2*inter][hidden], EGU [m*top_k][2*inter],
  * EHB [m*top_k][inter], down W [experts*hidden][inter], EY

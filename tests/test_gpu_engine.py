@@ -103,7 +103,7 @@ def test_moe_layer_through_picked_kernels(gpu):
     scores = hb.normal_bf16(23, 1.0, (rows, E))
     x = hb.normal_bf16(24, 1.0, (rows, H))
     with hb.Engine(gpu, "") as e:
-        layer = hb.MoeLayer(gpu, e, E, K_, H, MI, rows, Wgu, Wdn)
+        layer = hb.MoeLayer(gpu, e, E, K_, H, MI, rows, Wgu, Wdn, scores=scores, x=x)
         log = e.log()
     assert "[autotune] experts, 256 rows -> tiles of" in log
     assert re.search(r"\[autotune\] experts sort by 16 rows, 256 rows: scan .*atomic", log)

@@ -59,7 +59,7 @@ def sort_gpu(gpu, route, top_k, experts, bm, rows_max, atomic=False, m=None):
     return res[2], res[3]
 
 
-@pytest.mark.parametrize("bm", [16, 32, 64])
+@pytest.mark.parametrize("bm", [16, 32, 64, 128])
 def test_sort_bit_exact_and_atomic_invariants(gpu, bm):
     scores = hb.normal_bf16(0x5EED0005, 1.0, (T, E))
     route = orc.route(scores, TOPK)
@@ -123,10 +123,14 @@ EXPERT_TILES = {
     "m16_reg": dict(wm=1, wn=4, mfma=16, bn=128, bk=64, dbuf=0, lds_dma=0),
     "m32_reg_d": dict(wm=1, wn=4, mfma=16, bn=128, bk=64, dbuf=1, lds_dma=0),
     "m64_dma": dict(wm=1, wn=4, mfma=16, bn=256, bk=64, dbuf=1, lds_dma=1),
+    "m16_dma": dict(wm=1, wn=4, mfma=16, bn=128, bk=64, dbuf=1, lds_dma=1),
+    "m128_w2x2": dict(wm=2, wn=2, mfma=16, bn=128, bk=64, dbuf=1, lds_dma=1),
+    "m64_w2x4_s3": dict(wm=2, wn=4, mfma=16, bn=128, bk=64, dbuf=2, lds_dma=1),
 }
 
 
-@pytest.mark.parametrize("tname,bm", [("m16_reg", 16), ("m32_reg_d", 32), ("m64_dma", 64)])
+@pytest.mark.parametrize("tname,bm", [("m16_reg", 16), ("m32_reg_d", 32), ("m64_dma", 64),
+                                      ("m16_dma", 16), ("m128_w2x2", 128), ("m64_w2x4_s3", 64)])
 def test_grouped_gemm_gather_and_scatter(gpu, tname, bm):
     """Config 5's grouped gate|up (Gather: sorted row p reads X row
     list[p]/top_k) and down (Scatter: writes row list[p]), on 512 tokens
