@@ -6,6 +6,8 @@
 // qwen_kernels.rs route_qwen :1802, swiglu_slots :2087, moe_combine :2119),
 // with the kernel names following theirs (prefill.rs:1295-1300,
 // kernels.rs:960-975).
+#include <cctype>
+#include <cstdlib>
 #include <cstdio>
 
 #include "hb_internal.h"
@@ -60,7 +62,7 @@ hb_desc with_defaults(const hb_desc& in) {
     return d;
 }
 
-int emit(const hb_desc& d, Emitted* e) {
+static int emit_kind(const hb_desc& d, Emitted* e) {
     char name[256];
     e->defines.clear();
     switch (d.kind) {
@@ -248,6 +250,29 @@ int emit(const hb_desc& d, Emitted* e) {
         default:
             return fail(HB_ERR_UNSUPPORTED, "kernel kind " + std::to_string(d.kind) + " not built");
     }
+}
+
+// Kernel development: HB_DEV_DEFINES="-DX=1 -DY=2" adds defines to every
+// kernel built while it is set (a variant under study); the kernel's name
+// (its cache key) then carries them.  Unset in production.
+int emit(const hb_desc& d, Emitted* e) {
+    int rc = emit_kind(d, e);
+    const char* dev = getenv("HB_DEV_DEFINES");
+    if (rc || !dev || !*dev) return rc;
+    std::string tag = "_dev";
+    std::string cur;
+    for (const char* c = dev;; c++) {
+        if (*c == ' ' || *c == 0) {
+            if (!cur.empty()) e->defines.push_back(cur);
+            cur.clear();
+            if (!*c) break;
+            continue;
+        }
+        cur += *c;
+        tag += isalnum((unsigned char)*c) ? *c : '_';
+    }
+    e->name += tag;
+    return HB_OK;
 }
 
 uint32_t groups_of(const hb_desc& d, uint32_t m) {

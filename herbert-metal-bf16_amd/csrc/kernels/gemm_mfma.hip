@@ -95,8 +95,18 @@ typedef __attribute__((ext_vector_type(FM == 16 ? 4 : 16))) float acc_t;
 
 HB_DEV u32 lpos(u32 r, u32 c) { return r * CH + (c ^ ((r >> HB_SWZ) & (CH - 1))); }
 
+// HB_PROBE_SKIP (kernel development only; wrong results): bit 0 drops the
+// global loads, bit 1 the MFMAs (their operands kept live), bit 2 the LDS
+// fragment reads (the registers kept, opaque) -- to time each part alone.
+#ifndef HB_PROBE_SKIP
+#define HB_PROBE_SKIP 0
+#endif
+
 HB_DEV acc_t mfma(bf16x8 a, bf16x8 b, acc_t c) {
-#if HB_MFMA == 16
+#if HB_PROBE_SKIP & 2
+    asm volatile("" : "+v"(c) : "v"(a), "v"(b));
+    return c;
+#elif HB_MFMA == 16
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 #else
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -263,16 +273,23 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     const u32 fsw = (fr >> HB_SWZ) & (CH - 1);
     const u32 wbase = (wn * TN + fr) * CH, xbase = (wm * TM + fr) * CH;
     bf16x8 a[2][IN], b[2][IM];
+    auto frag = [&](bf16x8& dst, const u32x4* p) HB_INLINE {
+#if HB_PROBE_SKIP & 4
+        asm volatile("" : "+v"(dst));
+#else
+        dst = __builtin_bit_cast(bf16x8, *p);
+#endif
+    };
     // Step s's fragments of a stage into a[h], b[h]: IN of W (A operand), IM
     // of X (B operand).
     auto read_frags = [&](const u32x4* sX, const u32x4* sW, u32 s, u32 h) HB_INLINE {
         const u32 ch = (s * (KS / 8) + fc) ^ fsw;
 #pragma unroll
         for (u32 i = 0; i < IN; i++)
-            a[h][i] = __builtin_bit_cast(bf16x8, sW[wbase + ch + i * FM * CH]);
+            frag(a[h][i], &sW[wbase + ch + i * FM * CH]);
 #pragma unroll
         for (u32 j = 0; j < IM; j++)
-            b[h][j] = __builtin_bit_cast(bf16x8, sX[xbase + ch + j * FM * CH]);
+            frag(b[h][j], &sX[xbase + ch + j * FM * CH]);
     };
     auto mfmas = [&](u32 h) HB_INLINE {
 #pragma unroll
@@ -316,22 +333,31 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     auto lds_addr = [&](u32x4* p) HB_INLINE -> u32 {
         return (u32)(u64)(lds_u32x4*)p;
     };
-    auto load_stage = [&](u32 kt, u32x4* sX, u32x4* sW) HB_INLINE {
+    // Load q of K tile kt's stage: q < X_LD an X chunk, else a W chunk.
+    auto load_one = [&](u32 kt, u32x4* sX, u32x4* sW, u32 q) HB_INLINE {
         const u32 kb = kt * BK * 2;
-#pragma unroll
-        for (u32 q = 0; q < X_LD; q++)
+        if (HB_PROBE_SKIP & 1) return;
+        if (q < X_LD)
             asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                          :: "s"(lds_addr(&sX[q * NT + wave * 64])), "v"(xoff[q] * 2), "s"(rX),
                             "s"(kb) : "memory");
-#pragma unroll
-        for (u32 q = 0; q < W_LD; q++)
+        else
             asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                         :: "s"(lds_addr(&sW[q * NT + wave * 64])), "v"(woff[q] * 2), "s"(rW),
-                            "s"(kb) : "memory");
+                         :: "s"(lds_addr(&sW[(q - X_LD) * NT + wave * 64])),
+                            "v"(woff[q - X_LD] * 2), "s"(rW), "s"(kb) : "memory");
     };
     constexpr u32 LDT = X_LD + W_LD;  // load instructions per tile per lane
+    auto load_stage = [&](u32 kt, u32x4* sX, u32x4* sW) HB_INLINE {
+#pragma unroll
+        for (u32 q = 0; q < LDT; q++) load_one(kt, sX, sW, q);
+    };
     auto stx = [&](u32 i) HB_INLINE -> u32x4* { return sXa + i * XCHP; };
     auto stw = [&](u32 i) HB_INLINE -> u32x4* { return sWa + i * WCHP; };
+#if HB_PROBE_SKIP & 1
+    for (u32 i = tid; i < NS * XCHP; i += NT) sXa[i] = u32x4{i, 0, 0, 0};
+    for (u32 i = tid; i < NS * WCHP; i += NT) sWa[i] = u32x4{i, 0, 0, 0};
+    __syncthreads();
+#endif
     // Prologue: tiles 0..NS-2 in flight, tile 0 landed and published.
 #pragma unroll
     for (u32 t = 0; t + 1 < NS; t++)
@@ -401,6 +427,13 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
 #else
     u32x4 rx[X_LD], rw[W_LD];
     auto load = [&](u32 kt) HB_INLINE {
+#if HB_PROBE_SKIP & 1
+#pragma unroll
+        for (u32 q = 0; q < X_LD; q++) asm volatile("" : "+v"(rx[q]));
+#pragma unroll
+        for (u32 q = 0; q < W_LD; q++) asm volatile("" : "+v"(rw[q]));
+        return;
+#endif
 #pragma unroll
         for (u32 q = 0; q < X_LD; q++)
             if (XCH % NT == 0 || tid + q * NT < XCH) rx[q] = *(const u32x4*)(X + xoff[q] + kt * BK);
