@@ -10,7 +10,9 @@ picked at load (QwenEngine::gemm with gemm.auto, src/metal/qwen.rs:2200).
 `value` = the step's algorithmic flops (2*M*N*K summed) / its GPU time,
 inputs resident in HBM, timed with HIP events on the library's stream.
 
-Also reported: BASELINE config 5's MoE layer (the grouped expert GEMMs
+Also reported (not part of `value`): BASELINE config 1 (one GEMM, M=512),
+config 2 at M=512 and 1024, config 4 (27B-class shapes and lm_head at
+M=2048) under "prefill_more"; the decode steps at M=4 and 8; BASELINE config 5's MoE layer (the grouped expert GEMMs
 against HBM, and as TFLOP/s), and (the metric's second half) the decode matvec, M=1, over
 four layers of the same weights plus the lm_head (K=2560, N=151936), 2.2 GB
 streamed per step, as GB/s of algorithmic bytes (2*N*K + 2*M*K + 2*M*N per
@@ -48,6 +50,9 @@ M = 2048
 LAYER = [("qkv", 2560, 4608, 0), ("o", 4096, 2560, 2), ("gate_up", 2560, 18432, 0),
          ("down", 9216, 2560, 2)]
 LM_HEAD = ("lm_head", 2560, 151936, 0)
+CONFIG1 = [("gemm", 1024, 3584, 0)]
+CONFIG4 = [("qkv", 5120, 7168, 0), ("gate_up", 5120, 34816, 0), ("down", 17408, 5120, 2),
+           ("lm_head", 5120, 151936, 0)]
 DECODE_LAYERS = 4
 SEED = 0x5EED0002  # config 2's seeds: X = SEED + 2i, W = SEED + 2i + 1
 COPY_BYTES = 1 << 28  # the calibration copy of the traffic counters
@@ -88,6 +93,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-matvec", action="store_true")
     ap.add_argument("--no-moe", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--traffic-run", action="store_true")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     args = ap.parse_args()
@@ -122,12 +128,15 @@ def main():
         traffic_run(g, ops, per_gemm)
         return
 
-    # Warmup, then exactly K steps between two synchronisations, an event
-    # after every launch: the step time and each GEMM's mean launch time
-    # come from the same timed region.
+    # Warmup, then exactly K steps between two synchronisations (events at
+    # the ends only): the step time.  Then K more steps with an event after
+    # every launch: each GEMM's mean launch time (the gap an event adds
+    # between launches counts in it, so these are upper bounds).
     g.time_ops(ops, max(args.warmup, 0)) if args.warmup > 0 else None
     g.sync()
-    t, each = g.time_each(ops, args.steps)
+    t = g.time_ops(ops, args.steps)
+    g.sync()
+    t_ev, each = g.time_each(ops, args.steps)
     g.sync()
     ms = t / args.steps * 1e3
     value = flops / (t / args.steps) / 1e12
@@ -160,9 +169,13 @@ def main():
                                   "tflops": round(per_gemm[nm]["tflops"], 1)}
                              for nm, k, n, o in LAYER}},
         "roofline": roofline,
+        "ms_per_step_launch_events": round(t_ev / args.steps * 1e3, 4),
     }
     for b in bufs:
         g.free(b)
+
+    if not args.no_extra:
+        result["prefill_more"] = bench_prefill_more(g, e, hb, args.steps)
 
     if not args.no_matvec:
         result["matvec"] = bench_matvec(g, e, hb)
@@ -174,6 +187,46 @@ def main():
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_rows)
     print(json.dumps(result), flush=True)
+
+
+def gemm_set(g, e, hb, shapes, m, steps, seed):
+    """The GEMMs `shapes` [(name, K, N, out)] over m rows, each on the kernel
+    the selection layer picks, run back to back: the set's TFLOP/s and each
+    GEMM's (launch-event) time."""
+    state = g.alloc_with(np.array([0, 0, 0, m], np.uint32))
+    bufs, ops, flops = [state], [], []
+    for i, (name, k, n, out) in enumerate(shapes):
+        X = g.alloc_with(hb.normal_bf16(seed + 2 * i, 1.0, (m, k)))
+        W = g.alloc_with(hb.normal_bf16(seed + 2 * i + 1, 0.02, (n, k)))
+        Y = g.alloc_with(hb.normal_bf16(seed + 100 + i, 1.0, (m, n)))
+        bufs += [X, W, Y]
+        kern = e.gemm(k, n, out, hb.r(state), hb.r(W), hb.r(X), hb.r(Y), m)
+        ops.append(hb.Op(kern, [hb.r(state), hb.r(W), hb.r(X), hb.r(Y), hb.r(state), hb.r(state)], m))
+        flops.append(2.0 * m * n * k)
+    g.time_ops(ops, 2)
+    t = g.time_ops(ops, steps)
+    _, each = g.time_each(ops, steps)
+    out = {"m": m, "tflops": round(sum(flops) / (t / steps) / 1e12, 1),
+           "frac": round(sum(flops) / (t / steps) / 1e12 / MFMA_BF16_PEAK, 4),
+           "us": round(t / steps * 1e6, 2), "gemms": {}}
+    for (name, k, n, o), op, f, s in zip(shapes, ops, flops, each):
+        out["gemms"][name] = {"k": k, "n": n, "kernel": g.kernel_name(op.kernel), "us": round(s * 1e6, 2),
+                              "tflops": round(f / s / 1e12, 1), "frac": round(f / s / 1e12 / MFMA_BF16_PEAK, 4)}
+    for b in bufs:
+        g.free(b)
+    return out
+
+
+def bench_prefill_more(g, e, hb, steps):
+    """The other prefill cases of BASELINE.json: config 1 (one GEMM, M=512,
+    K=1024, N=3584), config 2 at M=512 and 1024 (the step above is M=2048),
+    config 4 (27B-class shapes at M=2048, lm_head included)."""
+    steps = max(3, min(steps, 10))
+    res = {"config1": gemm_set(g, e, hb, CONFIG1, 512, steps, 0x5EED0001)}
+    for m in (512, 1024):
+        res["config2_m%d" % m] = gemm_set(g, e, hb, LAYER, m, steps, SEED)
+    res["config4_m2048"] = gemm_set(g, e, hb, CONFIG4, M, steps, 0x5EED0004)
+    return res
 
 
 def traffic_run(g, ops, per_gemm):
@@ -280,44 +333,59 @@ def bench_moe(g, e, hb):
 
 
 def bench_matvec(g, e, hb):
-    """Decode step at M=1: DECODE_LAYERS layers of the 4 projections plus the
-    lm_head, each weight read once from HBM per step."""
-    out = {}
-    mv_m = 1
-    x_bufs = {}
-    ops, nbytes, tmp = [], 0.0, []
+    """Decode steps: DECODE_LAYERS layers of the 4
+    projections then the lm_head, in layer order, each weight read once from
+    HBM per step, at M = 1 (the reported value), 4 and 8 rows; the same
+    weights serve the three."""
+    ws = {}
     for name, k, n, o in LAYER + [LM_HEAD]:
         layers = 1 if name == "lm_head" else DECODE_LAYERS
-        ws = [g.alloc_with(hb.normal_bf16(0x5EED0003 + 17 * i + n, 0.02, (n, k))) for i in range(layers)]
-        if k not in x_bufs:
-            x_bufs[k] = g.alloc_with(hb.normal_bf16(0x5EED0003, 1.0, (mv_m, k)))
-        y = g.alloc_with(hb.normal_bf16(5, 1.0, (mv_m, n)))
-        tmp += ws + [y]
-        kern = e.mv(k, n, o, mv_m, [hb.r(w) for w in ws], hb.r(x_bufs[k]), hb.r(y))
-        for w in ws:
-            ops.append(hb.Op(kern, [hb.r(w), hb.r(x_bufs[k]), hb.r(y)], mv_m))
+        ws[name] = [g.alloc_with(hb.normal_bf16(0x5EED0003 + 17 * i + n, 0.02, (n, k)))
+                    for i in range(layers)]
+    tmp = [b for v in ws.values() for b in v]
+    res = {}
+    for mv_m in (1, 4, 8):
+        x_bufs, kern, ys = {}, {}, {}
+        for name, k, n, o in LAYER + [LM_HEAD]:
+            if k not in x_bufs:
+                x_bufs[k] = g.alloc_with(hb.normal_bf16(0x5EED0003, 1.0, (mv_m, k)))
+            ys[name] = g.alloc_with(hb.normal_bf16(5, 1.0, (mv_m, n)))
+            kern[name] = e.mv(k, n, o, mv_m, [hb.r(w) for w in ws[name]], hb.r(x_bufs[k]), hb.r(ys[name]))
+        ops, nbytes = [], 0.0
+        seq = [(nm, L) for L in range(DECODE_LAYERS) for nm in ("qkv", "o", "gate_up", "down")]
+        seq.append(("lm_head", 0))
+        shape = {nm: (k, n, o) for nm, k, n, o in LAYER + [LM_HEAD]}
+        for nm, L in seq:
+            k, n, o = shape[nm]
+            ops.append(hb.Op(kern[nm], [hb.r(ws[nm][L]), hb.r(x_bufs[k]), hb.r(ys[nm])], mv_m))
             nbytes += 2.0 * n * k + 2.0 * mv_m * k + 2.0 * mv_m * n * (2 if o == 2 else 1)
-        out[name] = g.kernel_name(kern)
-    g.time_ops(ops, 3)
-    reps = 20
-    t = g.time_ops(ops, reps) / reps
-    gbs = nbytes / t / 1e9
-    # the lm_head alone, two copies in turn (2 x 778 MB: no copy is still in
-    # the 256 MB last-level cache when it is read again)
-    k, n = LM_HEAD[1], LM_HEAD[2]
-    w2 = g.alloc_with(hb.normal_bf16(0x5EED0099, 0.02, (n, k)))
-    tmp.append(w2)
-    head2 = hb.Op(ops[-1].kernel, [hb.r(w2), ops[-1].bind[1], ops[-1].bind[2]], mv_m)
-    th = g.time_ops([ops[-1], head2], reps) / reps / 2
-    hb_bytes = 2.0 * LM_HEAD[1] * LM_HEAD[2] + 2.0 * mv_m * LM_HEAD[1] + 2.0 * mv_m * LM_HEAD[2]
-    for b in tmp + list(x_bufs.values()):
+        g.time_ops(ops, 3)
+        reps = 20
+        t = g.time_ops(ops, reps) / reps
+        gbs = nbytes / t / 1e9
+        r = {"value": round(gbs, 1), "unit": "GB/s", "frac": round(gbs / HBM_PEAK, 4), "peak": HBM_PEAK,
+             "ms_per_step": round(t * 1e3, 4), "m": mv_m, "layers": DECODE_LAYERS,
+             "bytes_per_step": nbytes, "kernels": {nm: g.kernel_name(kern[nm]) for nm in kern}}
+        if mv_m == 1:
+            # the lm_head alone, two copies in turn (2 x 778 MB: no copy is
+            # still in the 256 MB last-level cache when it is read again)
+            k, n = LM_HEAD[1], LM_HEAD[2]
+            w2 = g.alloc_with(hb.normal_bf16(0x5EED0099, 0.02, (n, k)))
+            tmp.append(w2)
+            head2 = hb.Op(ops[-1].kernel, [hb.r(w2), ops[-1].bind[1], ops[-1].bind[2]], mv_m)
+            th = g.time_ops([ops[-1], head2], reps) / reps / 2
+            hb_bytes = 2.0 * k * n + 2.0 * mv_m * k + 2.0 * mv_m * n
+            r["lm_head"] = {"gbs": round(hb_bytes / th / 1e9, 1), "us": round(th * 1e6, 2),
+                            "frac": round(hb_bytes / th / 1e9 / HBM_PEAK, 4)}
+        res[mv_m] = r
+        for b in list(x_bufs.values()) + list(ys.values()):
+            g.free(b)
+    for b in tmp:
         g.free(b)
-    return {"value": round(gbs, 1), "unit": "GB/s", "frac": round(gbs / HBM_PEAK, 4),
-            "peak": HBM_PEAK, "ms_per_step": round(t * 1e3, 4),
-            "config": {"m": mv_m, "layers": DECODE_LAYERS, "bytes_per_step": nbytes,
-                       "kernels": out},
-            "lm_head": {"gbs": round(hb_bytes / th / 1e9, 1), "us": round(th * 1e6, 2),
-                        "frac": round(hb_bytes / th / 1e9 / HBM_PEAK, 4)}}
+    out = res[1]
+    out["m4"] = {kk: res[4][kk] for kk in ("value", "frac", "ms_per_step", "kernels")}
+    out["m8"] = {kk: res[8][kk] for kk in ("value", "frac", "ms_per_step", "kernels")}
+    return out
 
 
 if __name__ == "__main__":

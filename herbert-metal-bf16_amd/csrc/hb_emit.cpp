@@ -162,20 +162,20 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
                           D("HB_BN", d.bn), D("HB_MFIRST", d.m_first ? 1 : 0)};
             return HB_OK;
         case HB_KIND_MATVEC: {
-            if (d.out > HB_OUT_RESIDUAL || d.form > 1)
+            if (d.out > HB_OUT_RESIDUAL || d.form > 2)
                 return fail(HB_ERR_INVALID, "matvec: out / form out of range");
             if (!d.k || !d.n || d.k % (8 * d.split) || (d.split != 1 && d.split != 2 && d.split != 4))
                 return fail(HB_ERR_UNSUPPORTED, "matvec: K a multiple of 8*split, split 1, 2 or 4");
-            if (d.form == 0 && (d.rows > 8 || !d.rows || d.rows * d.mv_m > 64 || d.mv_m > 16))
+            if (d.form != 1 && (d.rows > 8 || !d.rows || d.rows * d.mv_m > 64 || d.mv_m > 16))
                 return fail(HB_ERR_UNSUPPORTED, "matvec: rows 1..8, rows*m <= 64");
             if (d.form == 1 && (d.mv_m > 16 || (d.k / d.split) % 32))
                 return fail(HB_ERR_UNSUPPORTED, "matvec (MFMA): m <= 16, K/split a multiple of 32");
-            if (!d.unroll || d.unroll > 8)
-                return fail(HB_ERR_UNSUPPORTED, "matvec: unroll 1..8");
+            if (!d.unroll || d.unroll > (d.form == 1 ? 16u : 8u))
+                return fail(HB_ERR_UNSUPPORTED, "matvec: unroll 1..8 (MFMA form 1..16)");
             snprintf(name, sizeof name, "matvec_%ux%u%s_r%u_k%u%s_m%u_%s_u%u", d.k, d.n,
                      d.out == HB_OUT_F32 ? "_f32" : d.out == HB_OUT_RESIDUAL ? "_res" : "", d.rows,
                      d.split, d.persist ? ("_p" + std::to_string(d.persist)).c_str() : "", d.mv_m,
-                     d.form ? "mfma" : "valu", d.unroll);
+                     d.form == 1 ? "mfma" : d.form == 2 ? "dot2" : "valu", d.unroll);
             e->name = name;
             e->source = "matvec.hip";
             e->threads = 256;

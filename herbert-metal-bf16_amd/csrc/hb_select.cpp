@@ -779,11 +779,24 @@ int hb_engine_matvec(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, uint32_
                 std::string tag = (split > 1 ? "k" + std::to_string(split) : "") +
                                   (p ? "p" + std::to_string(p) : "");
                 add("r" + std::to_string(rows) + tag, desc(0, rows, split, p));
+                add("d" + std::to_string(rows) + tag, desc(2, rows, split, p));
+                if (rows <= 2) {
+                    // A whole row's chunks in one batch of loads when K /
+                    // split <= 4096: one HBM latency per wave, not two.
+                    hb_desc d8 = desc(mv_m > 1 ? 2 : 0, rows, split, p);
+                    d8.unroll = 8;
+                    add((mv_m > 1 ? "d" : "r") + std::to_string(rows) + tag + "u8", d8);
+                }
             }
     for (uint32_t split : splits)
         for (uint32_t p : pers) {
             std::string tag = (split > 1 ? "k" + std::to_string(split) : "") + (p ? "p" + std::to_string(p) : "");
             add("mfma" + tag, desc(1, 16, split, p));
+            for (uint32_t u : {8u, 16u}) {
+                hb_desc du = desc(1, 16, split, p);
+                du.unroll = u;
+                add("mfma_u" + std::to_string(u) + tag, du);
+            }
         }
     if (c.empty()) return fail(HB_ERR_COMPILE, std::string("matvec ") + key + ": no form built");
     std::vector<bool> all(c.size(), true);

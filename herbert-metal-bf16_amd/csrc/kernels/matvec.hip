@@ -9,18 +9,24 @@
 // (store).  The reference decodes one row; m up to MV_M is this build's
 // extension (one W read serves every row).
 //
-// Two forms (HB_FORM):
+// Three forms (HB_FORM):
 //  0 (VALU, the reference's arithmetic layout): a wavefront computes ROWS
 //    consecutive rows of W over its K range; lane l takes the 16-byte
 //    chunks l, l+64, ... of it, UNROLL chunks per row in flight; then a
 //    butterfly sum over the 64 lanes.
+//  2 (dot2): form 0's layout, each pair of products added by one
+//    v_dot2_f32_bf16 (bf16 operands straight from the loaded words, f32
+//    sum): half the VALU instructions of form 0 and no conversions -- the
+//    form for 4-8 rows, where form 0 runs out of VALU issue before HBM.
 //  1 (MFMA): a wavefront computes 16 rows of W with
 //    v_mfma_f32_16x16x32_bf16, W the A operand (the lane's 16-byte chunks
 //    loaded straight from memory as the operand, no conversion), x the B
-//    operand (rows past m are zeros).  Lane (r, q) of a step of 32 K holds
-//    row r's elements q*8*UNROLL + u*8.. of a UNROLL-step block, so each
-//    lane reads 16*UNROLL contiguous bytes; x uses the same K mapping.
-//    UNROLL independent accumulators, summed at the end.
+//    operand (rows past m are zeros).  Lane (r, q) holds row r's elements
+//    (u*4 + q)*8 .. +7 of step u of a UNROLL-step block, so one load
+//    instruction reads 64 contiguous bytes of each of the 16 rows (whole
+//    64-byte segments) and a block 64*UNROLL bytes of each row; x uses the
+//    same K mapping.
+//    Up to 4 independent accumulators, summed at the end.
 // Both: SPLIT wavefronts of a workgroup share a row block's K (contiguous
 // ranges); their partials are added in wave order through LDS.  PERSIST
 // > 0: that many workgroups loop over the row blocks.
@@ -34,7 +40,7 @@ constexpr int OUT = HB_OUT;
 constexpr u32 SPLIT = HB_SPLIT, U = HB_UNROLL;
 constexpr u32 WAVES = 4, NT = 256;
 constexpr u32 GROUPS_PER_WG = WAVES / SPLIT;  // row blocks per workgroup
-#if HB_FORM == 0
+#if HB_FORM != 1
 constexpr u32 RB = HB_ROWS;                   // rows per row block
 #else
 constexpr u32 RB = 16;
@@ -45,7 +51,7 @@ constexpr u32 KS = K / SPLIT;                 // K of one wave's range
 
 static_assert(WAVES % SPLIT == 0, "split divides the waves");
 static_assert(K % (8 * SPLIT) == 0 && KS % 8 == 0, "K split in whole chunks");
-static_assert(HB_FORM == 0 || (MV <= 16 && KS % 32 == 0), "MFMA form: m <= 16, K steps of 32");
+static_assert(HB_FORM != 1 || (MV <= 16 && KS % 32 == 0), "MFMA form: m <= 16, K steps of 32");
 
 HB_DEV void store_out(void* y, u64 at, float v) {
     if constexpr (OUT == 1) {
@@ -84,7 +90,7 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
     for (u32 wg = blockIdx.x; wg < nwg; wg += step) {
         const u32 blk = wg * GROUPS_PER_WG + gi;
         const u32 n0 = blk * RB;
-#if HB_FORM == 0
+#if HB_FORM != 1
         // ---- VALU: ROWS rows, lanes over 16-byte chunks ----
         float acc[RB][MV];
 #pragma unroll
@@ -118,18 +124,33 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
             for (u32 u = 0; u < U; u++) {
                 if (!decltype(full)::value && u * 64 >= REM) break;  // no lane has this chunk
                 const bool on = decltype(full)::value || (u * 64 + 64 <= REM) || (c0 + 64 * u < CHUNKS);
+                // Every x row's chunk loaded before the first sum (rows past
+                // m read row m-1, their sums never stored): one wait per
+                // chunk instead of one per x row.
+                u32x4 xs[MV];
 #pragma unroll
                 for (u32 j = 0; j < MV; j++) {
-                    if (j >= m) break;
-                    const u32x4 xv = on ? *(const u32x4*)(x + (u64)j * K + k0 + (c0 + 64 * u) * 8)
-                                        : u32x4{0u, 0u, 0u, 0u};
+                    const u32 jj = j < m ? j : m - 1;
+                    xs[j] = on ? *(const u32x4*)(x + (u64)jj * K + k0 + (c0 + 64 * u) * 8)
+                               : u32x4{0u, 0u, 0u, 0u};
+                }
+#pragma unroll
+                for (u32 j = 0; j < MV; j++) {
+                    const u32x4 xv = xs[j];
 #pragma unroll
                     for (u32 r = 0; r < RB; r++) {
                         float a = acc[r][j];
 #pragma unroll
                         for (u32 e = 0; e < 4; e++) {
+#if HB_FORM == 2
+                            // Inline asm: the builtin on words extracted from
+                            // these vectors was miscompiled (every e got e=0's
+                            // operands) by this image's compiler.
+                            asm volatile("v_dot2c_f32_bf16 %0, %1, %2" : "+v"(a) : "v"(wv[u][r][e]), "v"(xv[e]));
+#else
                             a = __builtin_fmaf(bf16_lo(wv[u][r][e]), bf16_lo(xv[e]), a);
                             a = __builtin_fmaf(bf16_hi(wv[u][r][e]), bf16_hi(xv[e]), a);
+#endif
                         }
                         acc[r][j] = a;
                     }
@@ -158,24 +179,25 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
         const u16* wrow = W + (u64)(n < N ? n : N - 1) * K + k0;
         const bool xon = fr < m;
         const u16* xrow = x + (u64)(xon ? fr : 0) * K + k0;
-        f32x4 acc[U];
+        constexpr u32 NA = U < 4 ? U : 4;  // independent accumulators
+        f32x4 acc[NA];
 #pragma unroll
-        for (u32 u = 0; u < U; u++) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (u32 u = 0; u < NA; u++) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
         constexpr u32 BLOCK = 32 * U;  // K per unrolled block
         u32 kk = 0;
         for (; kk + BLOCK <= KS; kk += BLOCK) {
             u32x4 wv[U], xv[U];
 #pragma unroll
             for (u32 u = 0; u < U; u++)
-                wv[u] = __builtin_nontemporal_load((const u32x4*)(wrow + kk + fq * 8 * U + u * 8));
+                wv[u] = __builtin_nontemporal_load((const u32x4*)(wrow + kk + (u * 4 + fq) * 8));
 #pragma unroll
             for (u32 u = 0; u < U; u++)
-                xv[u] = xon ? *(const u32x4*)(xrow + kk + fq * 8 * U + u * 8) : u32x4{0u, 0u, 0u, 0u};
+                xv[u] = xon ? *(const u32x4*)(xrow + kk + (u * 4 + fq) * 8) : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
             for (u32 u = 0; u < U; u++)
-                acc[u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wv[u]),
-                                                                 __builtin_bit_cast(bf16x8, xv[u]),
-                                                                 acc[u], 0, 0, 0);
+                acc[u % NA] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wv[u]),
+                                                                      __builtin_bit_cast(bf16x8, xv[u]),
+                                                                      acc[u % NA], 0, 0, 0);
         }
         for (; kk < KS; kk += 32) {
             const u32x4 wv = *(const u32x4*)(wrow + kk + fq * 8);
@@ -185,12 +207,12 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
                                                              0, 0, 0);
         }
 #pragma unroll
-        for (u32 u = 1; u < U; u++) acc[0] += acc[u];
+        for (u32 u = 1; u < NA; u++) acc[0] += acc[u];
         // Lane (fr, fq) holds rows 4*fq..+3 of the block for x row fr.
 #endif
 
         // ---- fold the SPLIT partials in wave order, then Out ----
-#if HB_FORM == 0
+#if HB_FORM != 1
         if constexpr (SPLIT > 1) {
             if (owner) part[(wave * RB + own_r) * 16 + own_j] = mine;
             __syncthreads();

@@ -113,7 +113,8 @@ typedef struct hb_desc {
     uint32_t bm, bn, bk, wm, wn, mfma, dbuf, swz, order;
     /* matvec: rows of x (1..16), waves sharing a row block's K (split),
      * persistent workgroups (0 = one per row block), W rows per wave
-     * (VALU form), form (0 VALU lanes-stride-K, 1 MFMA). */
+     * (VALU form), form (0 VALU lanes-stride-K, 1 MFMA, 2 the VALU layout with
+     * v_dot2_f32_bf16: two products added per instruction, no conversion). */
     uint32_t mv_m, split, persist, rows, form;
     /* MoE: slots per row (top_k), experts, the tile table's capacity
      * (moe_tiles, prefill.rs:832-835), rows of the largest block. */
@@ -122,7 +123,7 @@ typedef struct hb_desc {
      * into LDS (gfx950 global_load_lds_dwordx4). */
     uint32_t lds_dma;
     /* matvec: 16-byte chunks (VALU form) or 32-K MFMA steps (MFMA form)
-     * each lane keeps in flight per row; 0 = 4. */
+     * each lane keeps in flight per row (1..8; MFMA form 1..16); 0 = 4. */
     uint32_t unroll;
     /* GEMM tile order band (nax_tile_order, prefill.rs:615-631): 0 the
      * m_first walk; b > 0: consecutive workgroups walk every column tile of

@@ -52,10 +52,10 @@ def test_golden_gemm_simt_mm2d(gpu):
 
 
 @pytest.mark.parametrize("m", [1, 4])
-@pytest.mark.parametrize("form", [0, 1])
+@pytest.mark.parametrize("form", [0, 1, 2])
 def test_golden_matvec(gpu, m, form):
     x, w = G["mx%d" % m], G["mw%d" % m]
-    d = hb.matvec(128, 16, 0, mv_m=m, form=form, rows=16 if form else 2, split=2)
+    d = hb.matvec(128, 16, 0, mv_m=m, form=form, rows=16 if form == 1 else 2, split=2)
     res = launch(gpu, d, [w, x, m * 16 * 2], m, {2: (np.uint16, m * 16)})
     check_close(res[2].reshape(m, 16), G["my%d" % m], 128, abs_products(x, w), "matvec golden")
 

@@ -16,7 +16,11 @@ FORMS = {
     "valu_r4": dict(form=0, rows=4, split=1),
     "valu_r2_k4": dict(form=0, rows=2, split=4),
     "valu_r8_k2_p": dict(form=0, rows=8, split=2, persist=512),
+    "dot2_r2": dict(form=2, rows=2, split=1),
+    "dot2_r1_k2": dict(form=2, rows=1, split=2),
     "mfma_k1": dict(form=1, split=1),
+    "mfma_u8_k2": dict(form=1, split=2, unroll=8),
+    "mfma_u16": dict(form=1, split=1, unroll=16),
     "mfma_k4": dict(form=1, split=4),
     "mfma_k2_p": dict(form=1, split=2, persist=1024, unroll=2),
 }
@@ -56,7 +60,7 @@ def test_matvec_config3_layer(gpu, name, k, n, out, form, m):
 
 
 @pytest.mark.parametrize("m", [1, 8])
-@pytest.mark.parametrize("form", ["valu_r4", "mfma_k1"])
+@pytest.mark.parametrize("form", ["valu_r4", "dot2_r2", "mfma_k1"])
 def test_matvec_lm_head(gpu, form, m):
     """lm_head K=2560, N=151936 (778 MB of weights), all outputs checked."""
     k, n = 2560, 151936
