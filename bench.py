@@ -332,6 +332,58 @@ def bench_moe(g, e, hb):
     return out
 
 
+def decode_fused(g, e, hb, ws):
+    """The same M=1 decode step with the reference's decode fusions
+    (kernels.rs:236-290; qwen.rs:1311-1336): qkv reads the RMSNorm of the
+    residual stream (XSrc::Norm), gate|up too and writes the SwiGLU
+    (Out::Swiglu: nf outputs instead of 2*nf), down reads that, lm_head
+    reads the final norm: the norms and the SwiGLU cost no launch.  Bytes
+    as the plain step's, plus the norm weights, with gate|up's output nf
+    wide."""
+    eps = 1e-6
+    shape = {nm: (k, n, o) for nm, k, n, o in LAYER + [LM_HEAD]}
+    K = LAYER[0][1]
+    resid = g.alloc_with(hb.normal_bf16(0x5EED0021, 1.0, (1, K)))
+    nw = g.alloc_with(hb.normal_bf16(0x5EED0022, 0.1, (K,)))
+    attn = g.alloc_with(hb.normal_bf16(0x5EED0023, 1.0, (1, shape["o"][0])))
+    nf = shape["gate_up"][1] // 2
+    bufs = {"qkv": g.alloc(2 * shape["qkv"][1]), "o": g.alloc_with(hb.normal_bf16(7, 1.0, (1, K))),
+            "h": g.alloc(2 * nf), "down": g.alloc_with(hb.normal_bf16(8, 1.0, (1, K))),
+            "lm": g.alloc(2 * shape["lm_head"][1])}
+    r = hb.r
+    kq = e.mv_fused(K, shape["qkv"][1], hb.Out.Bf16, 1, [r(w) for w in ws["qkv"]], r(resid), r(bufs["qkv"]),
+                    xsrc=hb.XSrc.Norm, eps=eps, plus_one=True, norm_w=r(nw))
+    ko = e.mv(shape["o"][0], K, 2, 1, [r(w) for w in ws["o"]], r(attn), r(bufs["o"]))
+    kg = e.mv_fused(K, shape["gate_up"][1], hb.Out.Swiglu, 1, [r(w) for w in ws["gate_up"]], r(resid),
+                    r(bufs["h"]), xsrc=hb.XSrc.Norm, eps=eps, plus_one=True, norm_w=r(nw))
+    kd = e.mv(nf, K, 2, 1, [r(w) for w in ws["down"]], r(bufs["h"]), r(bufs["down"]))
+    kl = e.mv_fused(K, shape["lm_head"][1], hb.Out.Bf16, 1, [r(ws["lm_head"][0])], r(resid), r(bufs["lm"]),
+                    xsrc=hb.XSrc.Norm, eps=eps, plus_one=True, norm_w=r(nw))
+    ops, nbytes = [], 0.0
+    for L in range(DECODE_LAYERS):
+        ops.append(hb.Op(kq, [r(ws["qkv"][L]), r(resid), r(bufs["qkv"]), r(nw)], 1))
+        ops.append(hb.Op(ko, [r(ws["o"][L]), r(attn), r(bufs["o"])], 1))
+        ops.append(hb.Op(kg, [r(ws["gate_up"][L]), r(resid), r(bufs["h"]), r(nw)], 1))
+        ops.append(hb.Op(kd, [r(ws["down"][L]), r(bufs["h"]), r(bufs["down"])], 1))
+    ops.append(hb.Op(kl, [r(ws["lm_head"][0]), r(resid), r(bufs["lm"]), r(nw)], 1))
+    for nm, k, n, o in LAYER:
+        nout = n // 2 if nm == "gate_up" else n
+        per = 2.0 * n * k + 2.0 * k + 2.0 * nout * (2 if o == 2 else 1)
+        if nm in ("qkv", "gate_up"):
+            per += 2.0 * k  # the norm weights
+        nbytes += DECODE_LAYERS * per
+    k, n = LM_HEAD[1], LM_HEAD[2]
+    nbytes += 2.0 * n * k + 4.0 * k + 2.0 * n
+    g.time_ops(ops, 3)
+    reps = 20
+    t = g.time_ops(ops, reps) / reps
+    for b in [resid, nw, attn] + list(bufs.values()):
+        g.free(b)
+    gbs = nbytes / t / 1e9
+    return {"value": round(gbs, 1), "frac": round(gbs / HBM_PEAK, 4), "ms_per_step": round(t * 1e3, 4),
+            "kernels": {"qkv": g.kernel_name(kq), "gate_up": g.kernel_name(kg), "lm_head": g.kernel_name(kl)}}
+
+
 def bench_matvec(g, e, hb):
     """Decode steps: DECODE_LAYERS layers of the 4
     projections then the lm_head, in layer order, each weight read once from
@@ -380,9 +432,11 @@ def bench_matvec(g, e, hb):
         res[mv_m] = r
         for b in list(x_bufs.values()) + list(ys.values()):
             g.free(b)
+    res["fused"] = decode_fused(g, e, hb, ws)
     for b in tmp:
         g.free(b)
     out = res[1]
+    out["fused"] = res["fused"]
     out["m4"] = {kk: res[4][kk] for kk in ("value", "frac", "ms_per_step", "kernels")}
     out["m8"] = {kk: res[8][kk] for kk in ("value", "frac", "ms_per_step", "kernels")}
     return out

@@ -162,8 +162,14 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
                           D("HB_BN", d.bn), D("HB_MFIRST", d.m_first ? 1 : 0)};
             return HB_OK;
         case HB_KIND_MATVEC: {
-            if (d.out > HB_OUT_RESIDUAL || d.form > 2)
-                return fail(HB_ERR_INVALID, "matvec: out / form out of range");
+            if (d.out > HB_OUT_SWIGLU || d.form > 2 || d.xsrc > HB_XSRC_NORM)
+                return fail(HB_ERR_INVALID, "matvec: out / form / xsrc out of range");
+            if ((d.xsrc || d.out == HB_OUT_SWIGLU) && d.form == 1)
+                return fail(HB_ERR_UNSUPPORTED, "matvec: XSrc and Out::Swiglu fusions in the VALU forms");
+            if (d.out == HB_OUT_SWIGLU && (d.rows % 2 || d.n % 2))
+                return fail(HB_ERR_UNSUPPORTED, "matvec Out::Swiglu: even rows (gate and up) and n");
+            if (d.xsrc == HB_XSRC_NORM && ((uint64_t)d.mv_m * d.k * 2 > 65536 || d.k % 256))
+                return fail(HB_ERR_UNSUPPORTED, "matvec XSrc::Norm: m*k*2 <= 64 KiB of LDS, k a multiple of 256");
             if (!d.k || !d.n || d.k % (8 * d.split) || (d.split != 1 && d.split != 2 && d.split != 4))
                 return fail(HB_ERR_UNSUPPORTED, "matvec: K a multiple of 8*split, split 1, 2 or 4");
             if (d.form != 1 && (d.rows > 8 || !d.rows || d.rows * d.mv_m > 64 || d.mv_m > 16))
@@ -172,17 +178,23 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
                 return fail(HB_ERR_UNSUPPORTED, "matvec (MFMA): m <= 16, K/split a multiple of 32");
             if (!d.unroll || d.unroll > (d.form == 1 ? 16u : 8u))
                 return fail(HB_ERR_UNSUPPORTED, "matvec: unroll 1..8 (MFMA form 1..16)");
-            snprintf(name, sizeof name, "matvec_%ux%u%s_r%u_k%u%s_m%u_%s_u%u", d.k, d.n,
-                     d.out == HB_OUT_F32 ? "_f32" : d.out == HB_OUT_RESIDUAL ? "_res" : "", d.rows,
-                     d.split, d.persist ? ("_p" + std::to_string(d.persist)).c_str() : "", d.mv_m,
-                     d.form == 1 ? "mfma" : d.form == 2 ? "dot2" : "valu", d.unroll);
+            char xtag[48] = "";
+            if (d.xsrc == HB_XSRC_SWIGLU) snprintf(xtag, sizeof xtag, "_swi");
+            if (d.xsrc == HB_XSRC_NORM)
+                snprintf(xtag, sizeof xtag, "_nrm%08x%s", d.eps_bits, d.plus_one ? "p1" : "");
+            snprintf(name, sizeof name, "matvec_%ux%u%s%s_r%u_k%u%s_m%u_%s_u%u", d.k, d.n, xtag,
+                     d.out == HB_OUT_F32 ? "_f32" : d.out == HB_OUT_RESIDUAL ? "_res"
+                                                  : d.out == HB_OUT_SWIGLU ? "_sw" : "",
+                     d.rows, d.split, d.persist ? ("_p" + std::to_string(d.persist)).c_str() : "",
+                     d.mv_m, d.form == 1 ? "mfma" : d.form == 2 ? "dot2" : "valu", d.unroll);
             e->name = name;
             e->source = "matvec.hip";
             e->threads = 256;
-            e->nbind = 3;
+            e->nbind = d.xsrc == HB_XSRC_NORM ? 4 : 3;
             e->defines = {D("HB_K", d.k),         D("HB_N", d.n),          D("HB_OUT", d.out),
                           D("HB_MV_M", d.mv_m),   D("HB_FORM", d.form),    D("HB_ROWS", d.rows),
-                          D("HB_SPLIT", d.split), D("HB_PERSIST", d.persist), D("HB_UNROLL", d.unroll)};
+                          D("HB_SPLIT", d.split), D("HB_PERSIST", d.persist), D("HB_UNROLL", d.unroll),
+                          D("HB_XSRC", d.xsrc),   D("HB_EPS", d.eps_bits), D("HB_PLUS1", d.plus_one)};
             return HB_OK;
         }
         case HB_KIND_ROUTE:
@@ -287,9 +299,11 @@ uint32_t groups_of(const hb_desc& d, uint32_t m) {
             if (d.rows_of != HB_ROWS_DENSE) return d.tiles * nt;  // gemm_mma_expert_groups
             return cdiv(m, bm) * nt;                                 // gemm_mma_groups
         }
-        case HB_KIND_MATVEC: {  // matvec_groups / matvec_split_groups
+        case HB_KIND_MATVEC: {  // matvec_groups / matvec_split_groups / matvec_full_groups
             uint32_t rb = d.form == 1 ? 16 : d.rows, per = 4 / d.split;
-            uint32_t wgs = cdiv(cdiv(d.n, rb), per);
+            uint32_t n = d.n;
+            if (d.out == HB_OUT_SWIGLU) n /= 2, rb /= 2;  // output rows: gate rows
+            uint32_t wgs = cdiv(cdiv(n, rb), per);
             return d.persist ? (d.persist < wgs ? d.persist : wgs) : wgs;
         }
         case HB_KIND_ROUTE:
@@ -383,8 +397,10 @@ int check_bindings(const hb_desc& d, const uint64_t* s, uint32_t nbind, uint32_t
             return fail(HB_ERR_INVALID, "matvec of " + std::to_string(m) + " rows: 1.." +
                                             std::to_string(d.mv_m));
         if ((rc = need(s, 0, n * k * 2, "W"))) return rc;
-        if ((rc = need(s, 1, mm * k * 2, "x"))) return rc;
-        if ((rc = need(s, 2, mm * n * out_bytes(d.out), "y"))) return rc;
+        if ((rc = need(s, 1, mm * k * 2 * (d.xsrc == HB_XSRC_SWIGLU ? 2 : 1), "x"))) return rc;
+        uint64_t yn = d.out == HB_OUT_SWIGLU ? n / 2 : n;
+        if ((rc = need(s, 2, mm * yn * out_bytes(d.out), "y"))) return rc;
+        if (d.xsrc == HB_XSRC_NORM && (rc = need(s, 3, k * 2, "norm weights"))) return rc;
         return HB_OK;
     }
     return fail(HB_ERR_UNSUPPORTED, "kind " + std::to_string(d.kind));

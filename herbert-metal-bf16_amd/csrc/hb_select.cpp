@@ -305,7 +305,7 @@ hb_desc mm2d_desc(uint32_t k, uint32_t n, uint32_t out, bool mf, uint32_t tm, ui
 }
 
 const char* out_name(uint32_t out) {
-    return out == HB_OUT_F32 ? "F32" : out == HB_OUT_RESIDUAL ? "Residual" : "Bf16";
+    return out == HB_OUT_F32 ? "F32" : out == HB_OUT_RESIDUAL ? "Residual" : out == HB_OUT_SWIGLU ? "Swiglu" : "Bf16";
 }
 
 struct Cand {
@@ -315,6 +315,15 @@ struct Cand {
 };
 
 hb_op make_op(int32_t kernel, uint32_t m, std::initializer_list<hb_range> b) {
+    hb_op op{};
+    op.kernel = kernel;
+    op.m = m;
+    op.nbind = 0;
+    for (const auto& r : b) op.bind[op.nbind++] = r;
+    return op;
+}
+
+hb_op make_op(int32_t kernel, uint32_t m, const std::vector<hb_range>& b) {
     hb_op op{};
     op.kernel = kernel;
     op.m = m;
@@ -722,8 +731,18 @@ int hb_engine_gate_up(hb_engine* e, uint32_t h, uint32_t inter, hb_range state, 
 
 int hb_engine_matvec(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, uint32_t mv_m,
                      const hb_range* ws, uint32_t nws, hb_range x, hb_range y, int32_t* kernel) {
+    return hb_engine_matvec_fused(e, k, n, out, HB_XSRC_PLAIN, 0, 0, mv_m, ws, nws, x, y,
+                                  hb_range{}, kernel);
+}
+
+int hb_engine_matvec_fused(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, uint32_t xsrc,
+                           uint32_t eps_bits, uint32_t plus_one, uint32_t mv_m, const hb_range* ws,
+                           uint32_t nws, hb_range x, hb_range y, hb_range norm_w, int32_t* kernel) {
     const Tune& t = e->t;
     if (!nws) return fail(HB_ERR_INVALID, "matvec: no weights");
+    // A fusion (kernels.rs:236-290): the VALU forms, rows in gate/up pairs
+    // for Out::Swiglu (qwen.rs:1393-1397: rows.max(2)).
+    const bool fused = xsrc != HB_XSRC_PLAIN || out == HB_OUT_SWIGLU;
     auto desc = [&](uint32_t form, uint32_t rows, uint32_t split, uint32_t persist) {
         hb_desc d{};
         d.kind = HB_KIND_MATVEC;
@@ -736,11 +755,20 @@ int hb_engine_matvec(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, uint32_
         d.split = split;
         d.persist = persist;
         d.unroll = 4;
+        d.xsrc = xsrc;
+        d.eps_bits = eps_bits;
+        d.plus_one = plus_one;
         return d;
+    };
+    auto bind = [&](uint32_t i) {
+        std::vector<hb_range> b = {ws[i], x, y};
+        if (xsrc == HB_XSRC_NORM) b.push_back(norm_w);
+        return b;
     };
     if (!t["mv.auto"]) {
         // mv.split / mv.persist, the engine's rows (Options::matvec_rows).
         uint32_t rows = std::max<uint32_t>(1, std::min<uint32_t>(4, 64 / std::max<uint32_t>(mv_m, 1)));
+        if (out == HB_OUT_SWIGLU) rows = std::max<uint32_t>(rows, 2);
         return e->build(desc(0, rows, t["mv.split"], t["mv.persist"]), kernel);
     }
     std::string persists;
@@ -751,7 +779,10 @@ int hb_engine_matvec(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, uint32_
         persists += "]";
     }
     char key[160];
-    snprintf(key, sizeof key, "%ux%u %s m%u%s", k, n, out_name(out), mv_m, persists.c_str());
+    char xs[32] = "";
+    if (xsrc == HB_XSRC_SWIGLU) snprintf(xs, sizeof xs, " Swiglu");
+    if (xsrc == HB_XSRC_NORM) snprintf(xs, sizeof xs, " Norm(%08x%s)", eps_bits, plus_one ? ",+1" : "");
+    snprintf(key, sizeof key, "%ux%u%s %s m%u%s", k, n, xs, out_name(out), mv_m, persists.c_str());
     auto it = e->mv_pick.find(key);
     if (it != e->mv_pick.end()) return e->build(it->second, kernel);
     // Each form timed over every matrix of the shape (mv.cold) or the first.
@@ -761,6 +792,11 @@ int hb_engine_matvec(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, uint32_
     std::vector<uint32_t> splits = t["mv.splitauto"] ? std::vector<uint32_t>{1, 2, 4} : std::vector<uint32_t>{1};
     std::vector<uint32_t> pers = {0};
     for (uint32_t p : t.mv_persists) pers.push_back(p);
+    // XSrc::Norm computes the norm once per workgroup: persistent
+    // workgroups (two and four per CU) amortise it unless mv.persists names
+    // its own counts.
+    if (xsrc == HB_XSRC_NORM && t.mv_persists.empty())
+        for (uint32_t p : {512u, 1024u}) pers.push_back(p);
     auto add = [&](const std::string& name, const hb_desc& d) {
         int32_t kk;
         if (e->build(d, &kk)) {
@@ -768,7 +804,7 @@ int hb_engine_matvec(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, uint32_
             return;
         }
         std::vector<hb_op> ops;
-        for (uint32_t i = 0; i < nw; i++) ops.push_back(make_op(kk, mv_m, {ws[i], x, y}));
+        for (uint32_t i = 0; i < nw; i++) ops.push_back(make_op(kk, mv_m, bind(i)));
         c.push_back({name, kk, ops});
         descs.push_back(d);
     };
@@ -776,6 +812,7 @@ int hb_engine_matvec(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, uint32_
         for (uint32_t p : pers)
             for (uint32_t rows : {1u, 2u, 4u, 8u}) {
                 if (rows * mv_m > 64 || (p > 0 && rows == 8)) continue;
+                if (out == HB_OUT_SWIGLU && rows < 2) continue;
                 std::string tag = (split > 1 ? "k" + std::to_string(split) : "") +
                                   (p ? "p" + std::to_string(p) : "");
                 add("r" + std::to_string(rows) + tag, desc(0, rows, split, p));
@@ -790,6 +827,7 @@ int hb_engine_matvec(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, uint32_
             }
     for (uint32_t split : splits)
         for (uint32_t p : pers) {
+            if (fused) break;  // the fusions are VALU forms
             std::string tag = (split > 1 ? "k" + std::to_string(split) : "") + (p ? "p" + std::to_string(p) : "");
             add("mfma" + tag, desc(1, 16, split, p));
             for (uint32_t u : {8u, 16u}) {

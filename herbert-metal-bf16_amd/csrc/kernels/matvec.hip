@@ -31,8 +31,17 @@
 // ranges); their partials are added in wave order through LDS.  PERSIST
 // > 0: that many workgroups loop over the row blocks.
 //
+// Decode fusions (VALU forms, src/metal/kernels.rs:236-290, 640-975):
+// HB_XSRC 1 (XSrc::Swiglu): x holds [gate (K) | up (K)] per row, x =
+// bf16(g*sigmoid(g)*u) computed where it is loaded; HB_XSRC 2 (XSrc::Norm):
+// x is the residual stream, its RMSNorm (HB_EPS the epsilon's bits, HB_PLUS1)
+// computed into LDS first, the norm weights the 4th binding; HB_OUT 3
+// (Out::Swiglu): W holds [gate | up] rows, y = bf16(g*sigmoid(g)*u) of the
+// bf16-rounded sums, N/2 wide.
+//
 // Constants: HB_K, HB_N, HB_OUT, HB_MV_M, HB_FORM, HB_ROWS (form 0),
-// HB_SPLIT, HB_PERSIST, HB_UNROLL.  Bindings: W, x, y; then m (<= MV_M).
+// HB_SPLIT, HB_PERSIST, HB_UNROLL, HB_XSRC, HB_EPS, HB_PLUS1.  Bindings: W,
+// x, y[, norm weights]; then m (<= MV_M).
 #include "hb_common.h"
 
 constexpr u32 K = HB_K, N = HB_N, MV = HB_MV_M;
@@ -45,13 +54,33 @@ constexpr u32 RB = HB_ROWS;                   // rows per row block
 #else
 constexpr u32 RB = 16;
 #endif
-constexpr u32 WG_ROWS = RB * GROUPS_PER_WG;
-constexpr u32 NBLK = (N + RB - 1) / RB;
+#ifndef HB_XSRC
+#define HB_XSRC 0
+#endif
+#ifndef HB_EPS
+#define HB_EPS 0
+#endif
+#ifndef HB_PLUS1
+#define HB_PLUS1 0
+#endif
+// Out::Swiglu (HB_OUT 3): W's rows are [gate (N/2) | up (N/2)]; a row
+// block's RB rows are RB/2 gate rows and the same rows' up rows, and it
+// writes RB/2 outputs.
+constexpr bool SWO = OUT == 3;
+constexpr u32 NOUT = SWO ? N / 2 : N;         // output rows
+constexpr u32 RO = SWO ? RB / 2 : RB;         // output rows per row block
+constexpr u32 NBLK = (NOUT + RO - 1) / RO;
 constexpr u32 KS = K / SPLIT;                 // K of one wave's range
+static_assert(!SWO || (RB % 2 == 0 && N % 2 == 0 && HB_FORM != 1), "Out::Swiglu: VALU forms, even rows");
+static_assert(HB_XSRC == 0 || HB_FORM != 1, "XSrc fusions: VALU forms");
 
 static_assert(WAVES % SPLIT == 0, "split divides the waves");
 static_assert(K % (8 * SPLIT) == 0 && KS % 8 == 0, "K split in whole chunks");
 static_assert(HB_FORM != 1 || (MV <= 16 && KS % 32 == 0), "MFMA form: m <= 16, K steps of 32");
+
+// bf16(g * sigmoid(g) * u) as f32: swiglu's arithmetic (the SwiGLU kernels'
+// own expression, kernels.rs:256-261).
+HB_DEV float swiglu1(float g, float u) { return round_bf16((g * hb_sigmoid(g)) * u); }
 
 HB_DEV void store_out(void* y, u64 at, float v) {
     if constexpr (OUT == 1) {
@@ -77,19 +106,82 @@ HB_DEV float wave_sum(float v) {
 
 extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__ W,
                                                            const u16* __restrict__ x,
-                                                           void* __restrict__ y, u32 m_launch) {
+                                                           void* __restrict__ y,
+#if HB_XSRC == 2
+                                                           const u16* __restrict__ wn,
+#endif
+                                                           u32 m_launch) {
     __shared__ float part[SPLIT > 1 ? WAVES * RB * 16 : 1];
     const u32 tid = threadIdx.x, lane = tid & 63u;
     const u32 wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const u32 gi = wave / SPLIT, sp = wave % SPLIT;  // row block in the group, K part
     const u32 m = m_launch < MV ? m_launch : MV;
+#if HB_XSRC == 2
+    // XSrc::Norm (kernels.rs:355-440, rmsnorm :48-103): each x row's RMSNorm
+    // into LDS as bf16 before the matvec.  ss = sum of x^2: thread t's fma
+    // chain over elements t, t+256, ..., the 64 lanes' butterfly, then the 4
+    // waves' sums in wave order; m = ss * (1/K) + eps; inv = 1/sqrt(m)
+    // (correctly rounded); x' = bf16((x * inv) * w) with w + 1 for plus_one.
+    static_assert(K % 256 == 0 && MV * K * 2 <= 65536, "XSrc::Norm: K a multiple of 256, m*K*2 <= 64 KiB");
+    __shared__ u32x4 xn4[MV * K / 8];
+    __shared__ float nred[WAVES * MV];
+    {
+        constexpr u32 PER = K / 256;
+#pragma unroll
+        for (u32 j = 0; j < MV; j++) {
+            const u32 jj = j < m ? j : m - 1;
+            float a = 0.0f;
+            for (u32 i = 0; i < PER; i++) {
+                const float v = bf16_to_f32(x[(u64)jj * K + tid + i * 256]);
+                a = __builtin_fmaf(v, v, a);
+            }
+            a = wave_sum(a);
+            if (lane == 0) nred[wave * MV + j] = a;
+        }
+        __syncthreads();
+        const float inv_d = 1.0f / (float)K, eps = __uint_as_float((u32)HB_EPS);
+        u16* xn = (u16*)xn4;
+#pragma unroll
+        for (u32 j = 0; j < MV; j++) {
+            const u32 jj = j < m ? j : m - 1;
+            float ss = nred[j];
+#pragma unroll
+            for (u32 w = 1; w < WAVES; w++) ss = ss + nred[w * MV + j];
+            const float mm = ss * inv_d + eps;  // -ffp-contract=off: a mul, then an add
+            const float inv = __fdiv_rn(1.0f, __fsqrt_rn(mm));
+            for (u32 i = 0; i < PER; i++) {
+                const u32 c = tid + i * 256;
+                float wf = bf16_to_f32(wn[c]);
+                if (HB_PLUS1) wf = wf + 1.0f;
+                xn[j * K + c] = (u16)f32_to_bf16((bf16_to_f32(x[(u64)jj * K + c]) * inv) * wf);
+            }
+        }
+        __syncthreads();
+    }
+#endif
+    // 8 bf16 of x row jj at element `off` (XSrc: plain, swiglu'd, normed).
+    auto xload = [&](u32 jj, u32 off) HB_INLINE2 -> u32x4 {
+#if HB_XSRC == 2
+        return xn4[(jj * K + off) / 8];
+#elif HB_XSRC == 1
+        const u32x4 g = *(const u32x4*)(x + (u64)jj * 2 * K + off);
+        const u32x4 u = *(const u32x4*)(x + (u64)jj * 2 * K + K + off);
+        u32x4 h;
+#pragma unroll
+        for (u32 e = 0; e < 4; e++)
+            h[e] = pack_bf16x2(swiglu1(bf16_lo(g[e]), bf16_lo(u[e])), swiglu1(bf16_hi(g[e]), bf16_hi(u[e])));
+        return h;
+#else
+        return *(const u32x4*)(x + (u64)jj * K + off);
+#endif
+    };
     const u32 k0 = sp * KS;
     const u32 nwg = (NBLK + GROUPS_PER_WG - 1) / GROUPS_PER_WG;
     const u32 step = HB_PERSIST ? gridDim.x : nwg;
 
     for (u32 wg = blockIdx.x; wg < nwg; wg += step) {
         const u32 blk = wg * GROUPS_PER_WG + gi;
-        const u32 n0 = blk * RB;
+        const u32 n0 = blk * RO;  // first output row
 #if HB_FORM != 1
         // ---- VALU: ROWS rows, lanes over 16-byte chunks ----
         float acc[RB][MV];
@@ -100,8 +192,12 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
         const u16* wr[RB];
 #pragma unroll
         for (u32 r = 0; r < RB; r++) {
-            u32 n = n0 + r;
-            wr[r] = W + (u64)(n < N ? n : N - 1) * K;
+            // Out::Swiglu: rows RO.. are the up rows of rows 0..RO-1.
+            const u32 q = SWO && r >= RO ? r - RO : r;
+            u32 n = n0 + q;
+            n = n < NOUT ? n : NOUT - 1;
+            if (SWO && r >= RO) n += NOUT;
+            wr[r] = W + (u64)n * K;
         }
         // Blocks of 64*U chunks: lane l takes chunks l, l+64, ..., all U
         // loads of every row issued before the first fma; the last block
@@ -131,8 +227,7 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
 #pragma unroll
                 for (u32 j = 0; j < MV; j++) {
                     const u32 jj = j < m ? j : m - 1;
-                    xs[j] = on ? *(const u32x4*)(x + (u64)jj * K + k0 + (c0 + 64 * u) * 8)
-                               : u32x4{0u, 0u, 0u, 0u};
+                    xs[j] = on ? xload(jj, k0 + (c0 + 64 * u) * 8) : u32x4{0u, 0u, 0u, 0u};
                 }
 #pragma unroll
                 for (u32 j = 0; j < MV; j++) {
@@ -172,6 +267,15 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
                 if (lane == r * MV + j) mine = acc[r][j];
         const u32 own_r = lane / MV, own_j = lane % MV;
         const bool owner = lane < RB * MV;
+        // Out::Swiglu: the owner of gate row r also takes up row r + RO.
+        float mine_u = 0.0f;
+        if constexpr (SWO) {
+#pragma unroll
+            for (u32 r = 0; r < RO; r++)
+#pragma unroll
+                for (u32 j = 0; j < MV; j++)
+                    if (lane == r * MV + j) mine_u = acc[r + RO][j];
+        }
 #else
         // ---- MFMA: 16 rows x (m <= 16) columns per wave ----
         const u32 fr = lane & 15u, fq = lane >> 4;
@@ -217,14 +321,25 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
             if (owner) part[(wave * RB + own_r) * 16 + own_j] = mine;
             __syncthreads();
             if (sp == 0 && owner) {
-                float s = 0.0f;
+                float s = 0.0f, su = 0.0f;
 #pragma unroll
-                for (u32 q = 0; q < SPLIT; q++) s += part[((gi * SPLIT + q) * RB + own_r) * 16 + own_j];
+                for (u32 q = 0; q < SPLIT; q++) {
+                    s += part[((gi * SPLIT + q) * RB + own_r) * 16 + own_j];
+                    if (SWO && own_r < RO) su += part[((gi * SPLIT + q) * RB + own_r + RO) * 16 + own_j];
+                }
                 mine = s;
+                mine_u = su;
             }
         }
-        if (sp == 0 && owner && own_j < m && n0 + own_r < N)
+        if constexpr (SWO) {
+            // swiglu's bits: the gate and up sums as bf16, then bf16(g*sigmoid(g)*u)
+            // (kernels.rs:935-945).
+            if (sp == 0 && owner && own_r < RO && own_j < m && n0 + own_r < NOUT)
+                ((u16*)y)[(u64)own_j * NOUT + n0 + own_r] =
+                    (u16)f32_to_bf16(swiglu1(round_bf16(mine), round_bf16(mine_u)));
+        } else if (sp == 0 && owner && own_j < m && n0 + own_r < N) {
             store_out(y, (u64)own_j * N + n0 + own_r, mine);
+        }
 #else
         if constexpr (SPLIT > 1) {
 #pragma unroll

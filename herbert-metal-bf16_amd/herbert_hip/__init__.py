@@ -59,6 +59,14 @@ class Out(enum.IntEnum):
     Bf16 = 0
     F32 = 1
     Residual = 2
+    Swiglu = 3
+
+
+class XSrc(enum.IntEnum):
+    """XSrc (src/metal/kernels.rs:236-256): what a matvec's x holds."""
+    Plain = 0
+    Swiglu = 1
+    Norm = 2
 
 
 class Kind(enum.IntEnum):
@@ -95,12 +103,12 @@ class Range(ctypes.Structure):
 
 _DESC_FIELDS = ["kind", "k", "n", "out", "rows_of", "m_first", "bm", "bn", "bk", "wm", "wn",
                 "mfma", "dbuf", "swz", "order", "mv_m", "split", "persist", "rows", "form",
-                "top_k", "experts", "tiles", "rows_max", "lds_dma", "unroll", "band"]
+                "top_k", "experts", "tiles", "rows_max", "lds_dma", "unroll", "band", "xsrc", "eps_bits", "plus_one"]
 
 
 class Desc(ctypes.Structure):
     """hb_desc: a kernel's shape-keyed descriptor (what an emitter fixes)."""
-    _fields_ = [(f, ctypes.c_uint32) for f in _DESC_FIELDS] + [("reserved", ctypes.c_uint32 * 5)]
+    _fields_ = [(f, ctypes.c_uint32) for f in _DESC_FIELDS] + [("reserved", ctypes.c_uint32 * 2)]
 
     def __init__(self, **kw):
         super().__init__()
@@ -180,6 +188,9 @@ lib.hb_engine_gate_up.argtypes = [_P, _u32, _u32, Range, Range, Range, Range, Ra
                                   ctypes.POINTER(_i32), ctypes.POINTER(_i32)]
 lib.hb_engine_matvec.argtypes = [_P, _u32, _u32, _u32, _u32, ctypes.POINTER(Range), _u32, Range,
                                  Range, ctypes.POINTER(_i32)]
+lib.hb_engine_matvec_fused.argtypes = [_P, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
+                                       ctypes.POINTER(Range), _u32, Range, Range, Range,
+                                       ctypes.POINTER(_i32)]
 lib.hb_engine_experts.argtypes = [_P, _u32, _u32, _u32, _u32, _u32, ctypes.POINTER(MoeIo),
                                   ctypes.POINTER(_i32), ctypes.POINTER(_u32)]
 lib.hb_engine_autotune_seconds.argtypes = [_P]
@@ -257,11 +268,16 @@ def swiglu_rows(nf):
     return Desc(kind=Kind.SWIGLU, n=nf)
 
 
-def matvec(kdim, n, out, mv_m=1, rows=4, split=1, persist=0, form=0, unroll=4):
-    """matvec / matvec_split (kernels.rs:146, 502): y[m][n] = x[m][k].W^T for m <= mv_m;
-    form 0 the VALU layout (rows per wave), 1 the MFMA layout (16 rows per wave)."""
+def matvec(kdim, n, out, mv_m=1, rows=4, split=1, persist=0, form=0, unroll=4, xsrc=0, eps=0.0,
+           plus_one=False):
+    """matvec / matvec_split (kernels.rs:146, 502, 640): y[m][n] = x[m][k].W^T for m <= mv_m;
+    form 0 the VALU layout (rows per wave), 1 the MFMA layout (16 rows per wave), 2 the VALU
+    layout with v_dot2; xsrc / out Swiglu the decode fusions (VALU forms)."""
+    import struct
+    eps_bits = struct.unpack("<I", struct.pack("<f", eps))[0]
     return Desc(kind=Kind.MATVEC, k=kdim, n=n, out=out, mv_m=mv_m, rows=rows, split=split,
-                persist=persist, form=form, unroll=unroll)
+                persist=persist, form=form, unroll=unroll, xsrc=xsrc, eps_bits=eps_bits,
+                plus_one=1 if plus_one else 0)
 
 
 class Gpu:
@@ -450,6 +466,18 @@ class Engine:
         kern = _i32()
         check(lib.hb_engine_matvec(self.h, k, n, int(out), mv_m, arr, len(ws), x, y,
                                    ctypes.byref(kern)))
+        return kern.value
+
+    def mv_fused(self, k, n, out, mv_m, ws, x, y, xsrc=0, eps=0.0, plus_one=False, norm_w=None):
+        """mv_full with its fusions (qwen.rs:1311): xsrc XSrc.Swiglu / Norm
+        (eps, plus_one, the norm weights' Range), out Out.Swiglu."""
+        import struct
+        arr = (Range * len(ws))(*ws)
+        kern = _i32()
+        eps_bits = struct.unpack("<I", struct.pack("<f", eps))[0]
+        check(lib.hb_engine_matvec_fused(self.h, k, n, int(out), int(xsrc), eps_bits,
+                                         1 if plus_one else 0, mv_m, arr, len(ws), x, y,
+                                         norm_w if norm_w is not None else Range(), ctypes.byref(kern)))
         return kern.value
 
     def experts(self, experts, top_k, hidden, inter, m, io):

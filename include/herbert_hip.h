@@ -87,7 +87,18 @@ enum hb_kind {
 enum hb_out { /* Out (kernels.rs:30-43) */
     HB_OUT_BF16 = 0,
     HB_OUT_F32 = 1,
-    HB_OUT_RESIDUAL = 2
+    HB_OUT_RESIDUAL = 2,
+    /* matvec only: W holds [gate (n/2 rows) | up (n/2 rows)] and y[j] =
+     * bf16(g*sigmoid(g)*u) of the bf16-rounded gate and up sums, n/2 wide
+     * (Out::Swiglu, kernels.rs:655-660, 935-945) */
+    HB_OUT_SWIGLU = 3
+};
+
+enum hb_xsrc { /* XSrc (kernels.rs:236-256): what a matvec's x binding holds */
+    HB_XSRC_PLAIN = 0,  /* x [m][k] */
+    HB_XSRC_SWIGLU = 1, /* [gate (k) | up (k)] per row: x = bf16(g*sigmoid(g)*u) on load */
+    HB_XSRC_NORM = 2    /* the residual stream [m][k]: x = its RMSNorm (eps, plus_one, the
+                         * norm weights [k] at binding 3), computed into LDS first */
 };
 
 enum hb_rows { /* MmaRows (prefill.rs:317-338) */
@@ -130,7 +141,10 @@ typedef struct hb_desc {
      * b row tiles, those row tiles interleaved (the last band holds what is
      * left).  Dense rows only. */
     uint32_t band;
-    uint32_t reserved[5];
+    /* matvec: enum hb_xsrc; XSrc::Norm's epsilon (the f32's bits) and
+     * plus_one (weights used as w + 1). */
+    uint32_t xsrc, eps_bits, plus_one;
+    uint32_t reserved[2];
 } hb_desc;
 
 /* Gpu::pipeline(&Emitted) (metal/gpu.rs:127-148) for the kernel the
@@ -154,7 +168,7 @@ double hb_compile_seconds(hb_gpu *gpu);
  * context's stream: the bindings' sizes are checked against the descriptor
  * and m before anything runs.  Bindings per kind:
  *   GEMM, GEMM_DIRECT, GEMM_SIMT, GEMM_SWIGLU: state, W, X, Y[, list, tiles]
- *   MATVEC: W, x, y          ROUTE: scores, route
+ *   MATVEC: W, x, y[, norm weights (XSrc::Norm)]          ROUTE: scores, route
  *   SORT, SORT_ATOMIC: state, route, list, tiles
  *   GATHER: state, list, X, XS        SWIGLU: gate_up, h
  *   COMBINE: y, route, out    ROUND_PROBE: state (state[0] = chunk), out_int, out_hw
@@ -229,6 +243,14 @@ int hb_engine_gate_up(hb_engine *engine, uint32_t h, uint32_t inter, hb_range st
  * kept under "{k}x{n} {Out}"; else the form mv.split/mv.persist name. */
 int hb_engine_matvec(hb_engine *engine, uint32_t k, uint32_t n, uint32_t out, uint32_t mv_m,
                      const hb_range *ws, uint32_t nws, hb_range x, hb_range y, int32_t *kernel);
+/* mv_full with its decode fusions (qwen.rs:1311-1336: `out`, `xsrc`,
+ * `norm_w`): out may be HB_OUT_SWIGLU (W the [gate | up] rows, n their
+ * count), xsrc an enum hb_xsrc, with XSrc::Norm's epsilon bits, plus_one
+ * and its weights `norm_w` (bound 4th); the VALU forms only.  The pick is
+ * kept under "{k}x{n}{xsrc} {Out} m{mv_m}". */
+int hb_engine_matvec_fused(hb_engine *engine, uint32_t k, uint32_t n, uint32_t out, uint32_t xsrc,
+                           uint32_t eps_bits, uint32_t plus_one, uint32_t mv_m, const hb_range *ws,
+                           uint32_t nws, hb_range x, hb_range y, hb_range norm_w, int32_t *kernel);
 
 /* QwenEngine::expert_pipes (qwen.rs:2326-2391): the sort, the grouped
  * gate_up GEMM (Gather) and down GEMM (Scatter) of an MoE layer of `experts`

@@ -14,6 +14,9 @@
  *   - hbo_gemm / hbo_experts_gemm: f64 brute force at K where every
  *     summation order is exact, identity and permutation W, linearity, and
  *     committed fixtures;
+ *   - hbo_rmsnorm_rows: closed forms (constant rows: x' = w exactly; one
+ *     nonzero element), its two summation orders against each other, and
+ *     an f64 restatement within one bf16 ulp;
  *   - hbo_route / hbo_moe_sort / hbo_combine / hbo_swiglu: brute-force
  *     restatements in numpy (argsort with ties, set invariants, tile cover),
  *     and hbo_expf against libm within 2 ulp over a dense sweep.
@@ -372,6 +375,61 @@ void hbo_gemm_swiglu(const uint16_t *x, const uint16_t *w, uint16_t *h, int m, i
     hbo_gemm(x, w, gu, m, k, 2 * inter, HBO_OUT_BF16, threads);
     hbo_swiglu(gu, m, inter, h);
     free(gu);
+}
+
+/* ---- decode fusion XSrc::Norm (kernels.rs:48-103 rmsnorm, 355-440
+ * norm_into, 640-975 matvec_split_impl) ----------------------------------
+ * Each row of the residual stream x [m][k] normed: ss = sum of x^2, m =
+ * ss * f32(1/k) + eps (a multiply, then an add), inv = 1 / sqrt(m), x' =
+ * bf16((x * inv) * w') with w' = w (+ 1 for plus_one).  order 0 sums ss as
+ * the HIP kernel does (256 threads: thread t's fma chain over t, t+256, ...;
+ * the 64 lanes of each wave by the xor butterfly 32, 16, ..., 1; the 4
+ * waves' results added in wave order); order 1 sums in increasing index
+ * (one fma chain).  The reference's own order is Apple's simd_sum tree
+ * inside a threadgroup (parity with its bits unpinned). */
+void hbo_rmsnorm_rows(const uint16_t *x, const uint16_t *w, int m, int k, float eps, int plus_one,
+                      int order, uint16_t *out) {
+    const float inv_d = 1.0f / (float)k;
+    for (int j = 0; j < m; j++) {
+        const uint16_t *xr = x + (size_t)j * k;
+        float ss = 0.0f;
+        if (order == 1) {
+            for (int i = 0; i < k; i++) {
+                float v = hbo_bf16_to_f32(xr[i]);
+                ss = fmaf(v, v, ss);
+            }
+        } else {
+            float t[256], wave[4];
+            for (int th = 0; th < 256; th++) {
+                float a = 0.0f;
+                for (int i = th; i < k; i += 256) {
+                    float v = hbo_bf16_to_f32(xr[i]);
+                    a = fmaf(v, v, a);
+                }
+                t[th] = a;
+            }
+            for (int wv = 0; wv < 4; wv++) {
+                float l[64];
+                memcpy(l, t + 64 * wv, sizeof l);
+                for (int sh = 32; sh >= 1; sh >>= 1) {
+                    float nl[64];
+                    for (int i = 0; i < 64; i++) nl[i] = l[i] + l[i ^ sh];
+                    memcpy(l, nl, sizeof l);
+                }
+                wave[wv] = l[0];
+            }
+            ss = wave[0];
+            for (int wv = 1; wv < 4; wv++) ss = ss + wave[wv];
+        }
+        float mm = ss * inv_d;
+        mm = mm + eps;
+        float inv = 1.0f / sqrtf(mm);
+        for (int i = 0; i < k; i++) {
+            float wf = hbo_bf16_to_f32(w[i]);
+            if (plus_one) wf = wf + 1.0f;
+            out[(size_t)j * k + i] = hbo_f32_to_bf16((hbo_bf16_to_f32(xr[i]) * inv) * wf);
+        }
+    }
 }
 
 /* qwen_kernels.rs:2119-2165 (moe_combine): per token row, acc = 0, then for

@@ -149,6 +149,21 @@ def gemm_swiglu(x, w, inter, threads=None):
     return h
 
 
+lib.hbo_rmsnorm_rows.argtypes = [_P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_float, ctypes.c_int,
+                                 ctypes.c_int, _P]
+
+
+def rmsnorm_rows(x, w, eps, plus_one=False, order=0):
+    """XSrc::Norm's normed rows (hb_oracle.c hbo_rmsnorm_rows): order 0 the
+    HIP kernel's summation order, 1 increasing index."""
+    x = _c(x, np.uint16)
+    w = _c(w, np.uint16)
+    m, k = x.shape
+    out = np.zeros((m, k), np.uint16)
+    lib.hbo_rmsnorm_rows(_p(x), _p(w), m, k, float(eps), 1 if plus_one else 0, order, _p(out))
+    return out
+
+
 def combine(y, route_, top_k, d):
     y = _c(y, np.uint16)
     route_ = _c(route_, np.uint32)

@@ -92,6 +92,44 @@ def test_matvec_autotune_cold(gpu):
         gpu.free(b)
 
 
+def test_matvec_fused_autotune(gpu):
+    """mv_full with its fusions (qwen.rs:1311-1336): the pick of a decode
+    layer's gate|up with XSrc::Norm and Out::Swiglu, then the down with
+    XSrc::Swiglu, each logged under its key and computing the contract."""
+    k, nf, m, eps = 2560, 9216, 1, 1e-6
+    xr = hb.normal_bf16(31, 2.0, (m, k))
+    wn = hb.normal_bf16(32, 0.1, (k,))
+    wgu = hb.normal_bf16(33, 0.02, (2 * nf, k))
+    wd = hb.normal_bf16(34, 0.02, (k, nf))
+    gu = hb.normal_bf16(35, 1.0, (m, 2 * nf))
+    bufs = {nm: gpu.alloc_with(a) for nm, a in
+            (("xr", xr), ("wn", wn), ("wgu", wgu), ("wd", wd), ("gu", gu))}
+    H, Y = gpu.alloc(m * nf * 2), gpu.alloc(m * k * 2)
+    try:
+        with hb.Engine(gpu, "") as e:
+            k1 = e.mv_fused(k, 2 * nf, hb.Out.Swiglu, m, [hb.r(bufs["wgu"])], hb.r(bufs["xr"]), hb.r(H),
+                            xsrc=hb.XSrc.Norm, eps=eps, plus_one=True, norm_w=hb.r(bufs["wn"]))
+            k2 = e.mv_fused(nf, k, hb.Out.Bf16, m, [hb.r(bufs["wd"])], hb.r(bufs["gu"]), hb.r(Y),
+                            xsrc=hb.XSrc.Swiglu)
+            log = e.log()
+        assert re.search(r"\[autotune\] matvec 2560x18432 Norm\(358637bd,\+1\) Swiglu m1: r2 .* -> ", log), log
+        assert re.search(r"\[autotune\] matvec 9216x2560 Swiglu Bf16 m1: r1 .* -> ", log), log
+        assert "mfma" not in log.split("Norm(")[1].split("\n")[0]
+        gpu.launch(k1, [hb.r(bufs["wgu"]), hb.r(bufs["xr"]), hb.r(H), hb.r(bufs["wn"])], m)
+        h = gpu.download(H, np.uint16, m * nf).reshape(m, nf)
+        xn = orc.rmsnorm_rows(xr, wn, eps, True, 0)
+        ap = abs_products(xn, wgu)
+        check_close(h, orc.gemm_swiglu(xn, wgu, nf), k, np.maximum(ap[:, :nf], ap[:, nf:]) * 2,
+                    "fused gate_up pick", ulps=4.0)
+        gpu.launch(k2, [hb.r(bufs["wd"]), hb.r(bufs["gu"]), hb.r(Y)], m)
+        y = gpu.download(Y, np.uint16, m * k).reshape(m, k)
+        xs = orc.swiglu(gu, nf)
+        check_close(y, orc.gemm(xs, wd), nf, abs_products(xs, wd), "fused down pick")
+    finally:
+        for b in list(bufs.values()) + [H, Y]:
+            gpu.free(b)
+
+
 def test_moe_layer_through_picked_kernels(gpu):
     """expert_pipes picks sort, grouped GEMMs and tile rows; the whole routed
     layer through them equals the oracle's (route, sort, gather, GEMMs,

@@ -90,3 +90,96 @@ def test_matvec_rows_beyond_built_refused(gpu):
         gpu.launch(kern, [hb.r(W), hb.r(X), hb.r(Y)], 4)
     for b in (W, X, Y):
         gpu.free(b)
+
+
+# ---- decode fusions (kernels.rs:236-290, 355-440, 640-975): XSrc::Swiglu,
+# XSrc::Norm, Out::Swiglu.  Each is checked twice: within the contract of the
+# oracle's GEMM on the oracle's fused input (or fused output), and bit for
+# bit against the same matvec form run plain on that input (the fusion
+# changes where x comes from or how y is written, never a sum's order).
+
+FUSION_FORMS = {"valu_r2": dict(form=0, rows=2, split=1), "dot2_r4_k2": dict(form=2, rows=4, split=2),
+                "valu_r2_k4": dict(form=0, rows=2, split=4)}
+
+
+def run_mv_fused(gpu, x, w, out, y0, mv_m, extra=None, **form):
+    """The matvec with its fusion fields in `form`; extra: the norm weights."""
+    m = x.shape[0]
+    n = w.shape[0]
+    yn = n // 2 if out == hb.Out.Swiglu else n
+    esz = 4 if out == hb.Out.F32 else 2
+    bufs = [gpu.alloc_with(w), gpu.alloc_with(x),
+            gpu.alloc_with(y0) if y0 is not None else gpu.alloc(m * yn * esz)]
+    if extra is not None:
+        bufs.append(gpu.alloc_with(extra))
+    try:
+        kern = gpu.pipeline(hb.matvec(x.shape[1] // (2 if form.get("xsrc") == hb.XSrc.Swiglu else 1),
+                                      n, out, mv_m=mv_m, **form))
+        gpu.launch(kern, [hb.r(b) for b in bufs], m)
+        gpu.sync()
+        return gpu.download(bufs[2], np.float32 if out == hb.Out.F32 else np.uint16,
+                            m * yn).reshape(m, yn)
+    finally:
+        for b in bufs:
+            gpu.free(b)
+
+
+@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("form", sorted(FUSION_FORMS))
+def test_matvec_xsrc_swiglu(gpu, form, m):
+    """down with x = swiglu([gate | up]) on load: K=9216, N=2560, Residual."""
+    k, n = 9216, 2560
+    gu = hb.normal_bf16(0x5EED0011, 1.0, (m, 2 * k))
+    w = hb.normal_bf16(0x5EED0012, 0.02, (n, k))
+    y0 = hb.normal_bf16(13, 1.0, (m, n))
+    f = FUSION_FORMS[form]
+    got = run_mv_fused(gpu, gu, w, hb.Out.Residual, y0, 8, xsrc=hb.XSrc.Swiglu, **f)
+    xs = orc.swiglu(gu, k)
+    check_close(got, orc.gemm(xs, w, orc.OUT_RESIDUAL, y0), k, abs_products(xs, w),
+                "swiglu x %s m=%d" % (form, m), acc=orc.gemm(xs, w, orc.OUT_F32))
+    plain = run_mv_fused(gpu, xs, w, hb.Out.Residual, y0, 8, **f)
+    assert np.array_equal(got, plain), "XSrc::Swiglu differs from the plain matvec on swiglu(x)"
+
+
+@pytest.mark.parametrize("plus_one", [False, True])
+@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("form", sorted(FUSION_FORMS))
+def test_matvec_xsrc_norm(gpu, form, m, plus_one):
+    """qkv with x = RMSNorm(residual) computed into LDS first (eps 1e-6):
+    the normed input bit for bit the oracle's in the kernel's summation order
+    (shown by the plain matvec on the oracle's normed rows giving the same
+    bits), the output within the contract."""
+    k, n, eps = 2560, 4608, 1e-6
+    xr = hb.normal_bf16(0x5EED0013, 3.0, (m, k))
+    wn = hb.normal_bf16(0x5EED0014, 0.1, (k,))
+    w = hb.normal_bf16(0x5EED0015, 0.02, (n, k))
+    f = FUSION_FORMS[form]
+    got = run_mv_fused(gpu, xr, w, hb.Out.Bf16, None, 8, extra=wn, xsrc=hb.XSrc.Norm, eps=eps,
+                       plus_one=plus_one, **f)
+    xn = orc.rmsnorm_rows(xr, wn, eps, plus_one, 0)
+    check_close(got, orc.gemm(xn, w), k, abs_products(xn, w), "norm x %s m=%d" % (form, m))
+    plain = run_mv_fused(gpu, xn, w, hb.Out.Bf16, None, 8, **f)
+    assert np.array_equal(got, plain), "XSrc::Norm differs from the plain matvec on the oracle's norm"
+
+
+@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("form", sorted(FUSION_FORMS))
+def test_matvec_out_swiglu(gpu, form, m):
+    """gate|up with y = swiglu(rne(g), rne(u)): K=2560, W [gate 9216 | up
+    9216] rows, 9216 outputs.  The f32 sums of the same form (Out::F32) within
+    the contract of the oracle's, and the fused output == the oracle's
+    SwiGLU of those sums rounded, bit for bit; and within the contract of
+    the oracle's fused GEMM."""
+    k, nf = 2560, 9216
+    x = hb.normal_bf16(0x5EED0016, 1.0, (m, k))
+    w = hb.normal_bf16(0x5EED0017, 0.02, (2 * nf, k))
+    f = FUSION_FORMS[form]
+    got = run_mv_fused(gpu, x, w, hb.Out.Swiglu, None, 8, **f)
+    sums = run_mv_fused(gpu, x, w, hb.Out.F32, None, 8, **f)
+    ap = abs_products(x, w)
+    check_close(sums, orc.gemm(x, w, orc.OUT_F32), k, ap, "swiglu sums %s m=%d" % (form, m))
+    rs = hb.f32_to_bf16(sums)
+    want_bits = orc.swiglu(np.concatenate([rs[:, :nf], rs[:, nf:]], axis=1), nf)
+    assert np.array_equal(got, want_bits), "Out::Swiglu != swiglu of the rounded sums"
+    check_close(got, orc.gemm_swiglu(x, w, nf), k,
+                np.maximum(ap[:, :nf], ap[:, nf:]) * 2, "out swiglu %s m=%d" % (form, m), ulps=4.0)

@@ -299,3 +299,64 @@ def test_combine_order_and_rounding():
         c = bf16_to_f32(orc_f32_to_bf16((yf[:, s] * wf[:, s:s + 1]).astype(np.float32)))
         acc = bf16_to_f32(orc_f32_to_bf16((acc + c).astype(np.float32)))
     assert np.array_equal(got, orc_f32_to_bf16(acc))
+
+
+# ---- decode fusion XSrc::Norm (kernels.rs:48-103, 355-440) ---------------
+
+def _bf16(v):
+    return orc.lib.hbo_f32_to_bf16(float(v))
+
+
+def hb_normal(seed, std, shape):
+    """bf16 bits ~ N(0, std^2) from numpy's generator, rounded RNE."""
+    b = (np.random.default_rng(seed).normal(0.0, std, shape).astype(np.float32)).view(np.uint32)
+    return ((b + np.uint32(0x7FFF) + ((b >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)).astype(np.uint16)
+
+
+@pytest.mark.parametrize("plus_one", [False, True])
+def test_rmsnorm_constant_rows_are_the_weights(plus_one):
+    """x = 2 everywhere, k a power of two, eps = 0: ss = 4k exactly, m = 4,
+    inv = 1/2, so x' = bf16(1 * w') = w' (w + 1 rounded for plus_one), in
+    both summation orders."""
+    k = 2048
+    x = np.full((2, k), _bf16(2.0), np.uint16)
+    w = hb_normal(7, 0.5, k)
+    want = w if not plus_one else np.array([_bf16(float(v) + 1.0) for v in bf16_to_f32(w)],
+                                            np.uint16)
+    for order in (0, 1):
+        got = orc.rmsnorm_rows(x, w, 0.0, plus_one, order)
+        assert np.array_equal(got[0], want) and np.array_equal(got[1], want)
+
+
+def test_rmsnorm_one_nonzero_element():
+    """x = (c, 0, ..., 0) with c and k powers of two, eps = 0: ss = c^2, m =
+    c^2/k, sqrt(m) = |c|/sqrt(k) exact for k a power of 4, so x'_0 =
+    bf16(sign(c) sqrt(k) w_0) and x'_i = 0 elsewhere."""
+    k = 4096
+    for c in (0.5, -8.0, 2.0 ** -20):
+        x = np.zeros((1, k), np.uint16)
+        x[0, 0] = _bf16(c)
+        w = hb_normal(9, 1.0, k)
+        got = orc.rmsnorm_rows(x, w, 0.0, False, 0)
+        want0 = _bf16(math.copysign(64.0, c) * float(bf16_to_f32(w[:1])[0]))
+        assert got[0, 0] == want0 and not np.any(bf16_to_f32(got[0, 1:]))
+
+
+def test_rmsnorm_orders_and_f64_within_one_ulp():
+    """The kernel's summation order and the increasing-index order differ in
+    the last bits of ss only: x' within one bf16 ulp of each other and of an
+    f64 restatement; and the order matters (some elements differ)."""
+    m, k, eps = 6, 2560, 1e-6
+    x = hb_normal(11, 1.0, (m, k))
+    w = hb_normal(12, 0.1, k)
+    a = orc.rmsnorm_rows(x, w, eps, True, 0)
+    b = orc.rmsnorm_rows(x, w, eps, True, 1)
+    xf = bf16_to_f32(x).astype(np.float64)
+    wf = bf16_to_f32(w).astype(np.float64) + 1.0
+    ref = xf / np.sqrt((xf * xf).sum(axis=1, keepdims=True) / k + eps) * wf
+    for got in (a, b):
+        g = bf16_to_f32(got).astype(np.float64)
+        ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -126))) - 7)
+        assert np.all(np.abs(g - ref) <= ulp * 1.0001)
+    d = np.abs(bf16_to_f32(a).astype(np.float64) - bf16_to_f32(b))
+    assert np.all(d <= 2.0 ** (np.floor(np.log2(np.maximum(np.abs(bf16_to_f32(a)), 2.0 ** -126))) - 7))
