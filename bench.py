@@ -327,6 +327,25 @@ def bench_moe(g, e, hb):
     out["value"] = round((gu_b + dn_b) / (per["gate_up"] + per["down"]) / 1e9, 1)
     out["frac"] = round(out["value"] / HBM_PEAK, 4)
     layer.free()
+    # The whole sparse MLP (qwen.rs:2691-2732): post norm, shared expert
+    # (inter 512), router GEMM, the routed experts above, moe_out.
+    SI = 512
+    w = {"post_norm": g.alloc_with(hb.normal_bf16(seed + 4, 0.1, (H,))),
+         "router": g.alloc_with(hb.normal_bf16(seed + 5, 0.02, (E, H))),
+         "w_gate_up": wgu, "w_down": wdn,
+         "s_gate_up": g.alloc_with(hb.normal_bf16(seed + 6, 0.02, (2 * SI, H))),
+         "s_down": g.alloc_with(hb.normal_bf16(seed + 7, 0.02, (H, SI))),
+         "shared_gate": g.alloc_with(hb.normal_bf16(seed + 8, 0.05, (H,)))}
+    blk = hb.MoeBlock(g, e, E, TOPK, H, MI, SI, T, w, hb.normal_bf16(seed + 9, 1.0, (T, H)))
+    bops = blk.ops()
+    g.time_ops(bops, 3)
+    tb = g.time_ops(bops, reps) / reps
+    wbytes = 2.0 * used * 3 * MI * H + 2.0 * (E * H + 3 * SI * H + 2 * H)
+    out["block"] = {"us": round(tb * 1e6, 2), "weight_gbs": round(wbytes / tb / 1e9, 1),
+                    "ops": len(bops), "note": "post norm, shared expert, router, routed experts, moe_out"}
+    blk.free()
+    for nm in ("post_norm", "router", "s_gate_up", "s_down", "shared_gate"):
+        g.free(w[nm])
     g.free(wgu)
     g.free(wdn)
     return out

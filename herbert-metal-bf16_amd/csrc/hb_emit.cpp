@@ -253,6 +253,25 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
             e->nbind = 3;
             e->defines = {D("HB_OP", 6), D("HB_E", 64), D("HB_TOPK", d.top_k), D("HB_D", d.n)};
             return HB_OK;
+        case HB_KIND_MOE_OUT:
+            if (!d.n || d.n % 256) return fail(HB_ERR_UNSUPPORTED, "moe_out: d a multiple of 256");
+            snprintf(name, sizeof name, "moe_out_%u", d.n);
+            e->name = name;
+            e->source = "moe.hip";
+            e->threads = 256;
+            e->nbind = 5;
+            e->defines = {D("HB_OP", 7), D("HB_E", 64), D("HB_TOPK", 1), D("HB_D", d.n)};
+            return HB_OK;
+        case HB_KIND_RMSNORM:
+            if (!d.n || d.n % 256) return fail(HB_ERR_UNSUPPORTED, "rmsnorm: d a multiple of 256");
+            snprintf(name, sizeof name, "rmsnorm_%u_e%08x%s", d.n, d.eps_bits, d.plus_one ? "_p1" : "");
+            e->name = name;
+            e->source = "moe.hip";
+            e->threads = 256;
+            e->nbind = 3;
+            e->defines = {D("HB_OP", 8), D("HB_E", 64), D("HB_TOPK", 1), D("HB_D", d.n),
+                          D("HB_EPS", d.eps_bits), D("HB_PLUS1", d.plus_one)};
+            return HB_OK;
         case HB_KIND_ROUND_PROBE:
             e->name = "round_probe_bf16";
             e->source = "probe.hip";
@@ -316,6 +335,9 @@ uint32_t groups_of(const hb_desc& d, uint32_t m) {
         case HB_KIND_SWIGLU:
         case HB_KIND_COMBINE:
             return (uint32_t)(((uint64_t)m * (d.n / 8) + 255) / 256);
+        case HB_KIND_MOE_OUT:
+        case HB_KIND_RMSNORM:
+            return m;  // a workgroup per row
         case HB_KIND_ROUND_PROBE:
             return (1u << 24) / 256;  // one pattern per thread
         default:
@@ -384,6 +406,16 @@ int check_bindings(const hb_desc& d, const uint64_t* s, uint32_t nbind, uint32_t
             if ((rc = need(s, 0, 16, "state"))) return rc;
             if ((rc = need(s, 1, 2ull << 24, "out_int"))) return rc;
             return need(s, 2, 2ull << 24, "out_hw");
+        case HB_KIND_RMSNORM:
+            if ((rc = need(s, 0, mm * d.n * 2, "x"))) return rc;
+            if ((rc = need(s, 1, (uint64_t)d.n * 2, "w"))) return rc;
+            return need(s, 2, mm * d.n * 2, "y");
+        case HB_KIND_MOE_OUT:
+            if ((rc = need(s, 0, mm * d.n * 2, "xn"))) return rc;
+            if ((rc = need(s, 1, (uint64_t)d.n * 2, "shared_gate"))) return rc;
+            if ((rc = need(s, 2, mm * d.n * 2, "experts"))) return rc;
+            if ((rc = need(s, 3, mm * d.n * 2, "shared"))) return rc;
+            return need(s, 4, mm * d.n * 2, "x");
         case HB_KIND_COMBINE:
             if ((rc = need(s, 0, mm * d.top_k * d.n * 2, "y"))) return rc;
             if ((rc = need(s, 1, mm * k2 * 4, "route"))) return rc;

@@ -9,10 +9,19 @@
 //   4 gather  (src/metal/prefill.rs:579-610, moe_gather)
 //   5 swiglu  (src/metal/qwen_kernels.rs:2087-2117, swiglu_slots)
 //   6 combine (src/metal/qwen_kernels.rs:2119-2165, moe_combine)
+//   7 moe_out (src/metal/qwen_kernels.rs:2163-2214: the shared expert's
+//             gate, the experts' and shared sums, the residual add)
+//   8 rmsnorm (src/metal/kernels.rs:48-103: the block's input norm)
 // Constants: HB_OP, HB_E (experts), HB_TOPK, HB_BM (rows per expert tile),
 // HB_TILES (table capacity), HB_D (row width: hidden, or n of SwiGLU).
 #include "hb_common.h"
 
+#ifndef HB_EPS
+#define HB_EPS 0
+#endif
+#ifndef HB_PLUS1
+#define HB_PLUS1 0
+#endif
 constexpr u32 E = HB_E, TOPK = HB_TOPK, D = HB_D;
 
 #if HB_OP == 1
@@ -271,5 +280,71 @@ extern "C" __global__ __launch_bounds__(256) void HB_NAME(const u32x4* __restric
 #pragma unroll
     for (u32 e = 0; e < 4; e++) o[e] = pack_bf16x2(acc[2 * e], acc[2 * e + 1]);
     out[i] = o;
+}
+
+#elif HB_OP == 7
+// ---- moe_out (qwen_kernels.rs:2163-2214): the end of the sparse MoE block
+// and the residual add, a workgroup per row: g = bf16(sigmoid(bf16(gate .
+// xn))), x = bf16(x + bf16(experts + bf16(g * shared))).  The dot: thread
+// t's fma chain over elements t, t+256, ..., the 64 lanes' butterfly, the 4
+// waves' sums in wave order (the oracle restates this order). ----
+static_assert(D % 256 == 0, "moe_out: d a multiple of 256");
+
+extern "C" __global__ __launch_bounds__(256) void HB_NAME(const u16* __restrict__ xn,
+                                                            const u16* __restrict__ gate,
+                                                            const u16* __restrict__ ex,
+                                                            const u16* __restrict__ sh,
+                                                            u16* __restrict__ x, u32 rows) {
+    __shared__ float red[4];
+    const u32 r = blockIdx.x, t = threadIdx.x, lane = t & 63u;
+    if (r >= rows) return;
+    const u64 base = (u64)r * D;
+    float a = 0.0f;
+    for (u32 i = t; i < D; i += 256) a = __builtin_fmaf(bf16_to_f32(xn[base + i]), bf16_to_f32(gate[i]), a);
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) a += __shfl_xor(a, s, 64);
+    if (lane == 0) red[t >> 6] = a;
+    __syncthreads();
+    const float dot = ((red[0] + red[1]) + red[2]) + red[3];
+    const float g = round_bf16(hb_sigmoid(round_bf16(dot)));
+    for (u32 i = t; i < D; i += 256) {
+        const float s = round_bf16(g * bf16_to_f32(sh[base + i]));
+        const float o = round_bf16(bf16_to_f32(ex[base + i]) + s);
+        x[base + i] = (u16)f32_to_bf16(bf16_to_f32(x[base + i]) + o);
+    }
+}
+
+#elif HB_OP == 8
+// ---- rmsnorm (kernels.rs:48-103), a workgroup per row: ss = sum of x^2
+// (thread t's fma chain over t, t+256, ..., the 64-lane butterfly, the 4
+// waves in order), m = ss * f32(1/D) + eps, inv = 1/sqrt(m) correctly
+// rounded, y = bf16((x * inv) * w) with w + 1 for plus_one -- the same
+// arithmetic as the matvec's fused XSrc::Norm. ----
+static_assert(D % 256 == 0, "rmsnorm: d a multiple of 256");
+
+extern "C" __global__ __launch_bounds__(256) void HB_NAME(const u16* __restrict__ x,
+                                                            const u16* __restrict__ w,
+                                                            u16* __restrict__ y, u32 rows) {
+    __shared__ float red[4];
+    const u32 r = blockIdx.x, t = threadIdx.x, lane = t & 63u;
+    if (r >= rows) return;
+    const u64 base = (u64)r * D;
+    float a = 0.0f;
+    for (u32 i = t; i < D; i += 256) {
+        const float v = bf16_to_f32(x[base + i]);
+        a = __builtin_fmaf(v, v, a);
+    }
+#pragma unroll
+    for (int s = 32; s >= 1; s >>= 1) a += __shfl_xor(a, s, 64);
+    if (lane == 0) red[t >> 6] = a;
+    __syncthreads();
+    const float ss = ((red[0] + red[1]) + red[2]) + red[3];
+    const float inv_d = 1.0f / (float)D, eps = __uint_as_float((u32)HB_EPS);
+    const float inv = __fdiv_rn(1.0f, __fsqrt_rn(ss * inv_d + eps));
+    for (u32 i = t; i < D; i += 256) {
+        float wf = bf16_to_f32(w[i]);
+        if (HB_PLUS1) wf = wf + 1.0f;
+        y[base + i] = (u16)f32_to_bf16((bf16_to_f32(x[base + i]) * inv) * wf);
+    }
 }
 #endif

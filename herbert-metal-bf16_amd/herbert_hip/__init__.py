@@ -82,6 +82,8 @@ class Kind(enum.IntEnum):
     SWIGLU = 9
     COMBINE = 10
     ROUND_PROBE = 11
+    MOE_OUT = 12
+    RMSNORM = 13
 
 
 class Rows(enum.IntEnum):
@@ -555,3 +557,82 @@ class MoeLayer:
         for name, buf in self.buf.items():
             if name not in ("w_gate_up", "w_down"):
                 self.gpu.free(buf)
+
+
+def rmsnorm(d, eps, plus_one=False):
+    """rmsnorm (kernels.rs:48-103): y = bf16(x / sqrt(mean(x^2) + eps) * w) per row of d."""
+    import struct
+    eps_bits = struct.unpack("<I", struct.pack("<f", eps))[0]
+    return Desc(kind=Kind.RMSNORM, n=d, eps_bits=eps_bits, plus_one=1 if plus_one else 0)
+
+
+def moe_out(d):
+    """moe_out (qwen_kernels.rs:2163-2214): x = bf16(x + bf16(experts + bf16(g * shared)))
+    with g = bf16(sigmoid(bf16(shared_gate . xn))), in place, a row per workgroup."""
+    return Desc(kind=Kind.MOE_OUT, n=d)
+
+
+class MoeBlock:
+    """The sparse MLP of a qwen3_5_moe layer over blocks of up to `rows` rows,
+    in the reference's op order (qwen.rs:2691-2732): the post norm (x ->
+    xn), the shared expert (gate|up GEMM [+ SwiGLU] and down, gate_up_pipes
+    and gemm picks), the router GEMM (xn -> scores), the routed experts
+    (MoeLayer: route, sort, [gather], grouped gate|up, SwiGLU, grouped down,
+    combine -> esum), moe_out (x += experts + gated shared output).
+
+    `w`: device buffers {"post_norm": [h], "router": [E][h], "w_gate_up":
+    [E*2*inter][h], "w_down": [E*h][inter], "s_gate_up": [2*si][h], "s_down":
+    [h][si], "shared_gate": [h]}.  `x` (host [rows][h]) is the residual
+    stream the selection runs on; the block updates buf["x"] in place."""
+
+    def __init__(self, gpu, engine, experts, top_k, hidden, inter, shared_inter, rows, w, x,
+                 eps=1e-6, plus_one=True):
+        g, h, si = gpu, hidden, shared_inter
+        self.gpu, self.rows, self.h, self.si, self.w = gpu, rows, h, si, w
+        self.buf = {"state": g.alloc_with(np.array([0, 0, 0, rows], np.uint32)),
+                    "x": g.alloc_with(x),
+                    "s_gu": g.alloc(rows * 2 * si * 2), "s_h": g.alloc(rows * si * 2),
+                    "sout": g.alloc(rows * h * 2)}
+        b = self.buf
+        self.norm_k = g.pipeline(rmsnorm(h, eps, plus_one))
+        self.out_k = g.pipeline(moe_out(h))
+        # xn and the router's scores on the selection's input, for the
+        # experts' timing on a real route (the reference's real_route).
+        xn_t, sc_t = g.alloc(rows * h * 2), g.alloc(rows * experts * 2)
+        g.launch(self.norm_k, [r(b["x"]), r(w["post_norm"]), r(xn_t)], rows)
+        self.router_k = engine.gemm(h, experts, Out.Bf16, r(b["state"]), r(w["router"]), r(xn_t),
+                                    r(sc_t), rows)
+        g.launch(self.router_k, [r(b["state"]), r(w["router"]), r(xn_t), r(sc_t), r(b["state"]),
+                                 r(b["state"])], rows)
+        g.sync()
+        xn = g.download(xn_t, np.uint16, rows * h).reshape(rows, h)
+        scores = g.download(sc_t, np.uint16, rows * experts).reshape(rows, experts)
+        g.free(xn_t)
+        g.free(sc_t)
+        self.layer = MoeLayer(g, engine, experts, top_k, h, inter, rows, w["w_gate_up"], w["w_down"],
+                              scores=scores, x=xn)
+        L = self.layer.buf
+        self.s_gu_k, self.s_sw_k = engine.gate_up(h, si, r(b["state"]), r(w["s_gate_up"]), r(L["x"]),
+                                                  r(b["s_gu"]), r(b["s_h"]), rows)
+        self.s_dn_k = engine.gemm(si, h, Out.Bf16, r(b["state"]), r(w["s_down"]), r(b["s_h"]),
+                                  r(b["sout"]), rows)
+
+    def ops(self, m=None):
+        m = self.rows if m is None else m
+        b, L, w, st = self.buf, self.layer.buf, self.w, r(self.buf["state"])
+        ops = [Op(self.norm_k, [r(b["x"]), r(w["post_norm"]), r(L["x"])], m)]
+        if self.s_sw_k >= 0:
+            ops.append(Op(self.s_gu_k, [st, r(w["s_gate_up"]), r(L["x"]), r(b["s_gu"]), st, st], m))
+            ops.append(Op(self.s_sw_k, [r(b["s_gu"]), r(b["s_h"])], m))
+        else:
+            ops.append(Op(self.s_gu_k, [st, r(w["s_gate_up"]), r(L["x"]), r(b["s_h"]), st, st], m))
+        ops.append(Op(self.s_dn_k, [st, r(w["s_down"]), r(b["s_h"]), r(b["sout"]), st, st], m))
+        ops.append(Op(self.router_k, [st, r(w["router"]), r(L["x"]), r(L["scores"]), st, st], m))
+        ops += self.layer.ops(m)
+        ops.append(Op(self.out_k, [r(L["x"]), r(w["shared_gate"]), r(L["out"]), r(b["sout"]), r(b["x"])], m))
+        return ops
+
+    def free(self):
+        self.layer.free()
+        for buf in self.buf.values():
+            self.gpu.free(buf)

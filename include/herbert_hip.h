@@ -81,7 +81,9 @@ enum hb_kind {
     HB_KIND_GATHER = 8,      /* moe_gather (prefill.rs:579-610) */
     HB_KIND_SWIGLU = 9,      /* swiglu_slots / swiglu_rows (qwen_kernels.rs:2087-2117) */
     HB_KIND_COMBINE = 10,    /* moe_combine (qwen_kernels.rs:2119-2165) */
-    HB_KIND_ROUND_PROBE = 11 /* herbert-metal-probe round (bin/herbert-metal-probe.rs:7-11) */
+    HB_KIND_ROUND_PROBE = 11, /* herbert-metal-probe round (bin/herbert-metal-probe.rs:7-11) */
+    HB_KIND_MOE_OUT = 12,    /* moe_out (qwen_kernels.rs:2163-2214): the MoE block's end */
+    HB_KIND_RMSNORM = 13     /* rmsnorm (kernels.rs:48-103): the block's input norm, rows of n */
 };
 
 enum hb_out { /* Out (kernels.rs:30-43) */
@@ -172,6 +174,8 @@ double hb_compile_seconds(hb_gpu *gpu);
  *   SORT, SORT_ATOMIC: state, route, list, tiles
  *   GATHER: state, list, X, XS        SWIGLU: gate_up, h
  *   COMBINE: y, route, out    ROUND_PROBE: state (state[0] = chunk), out_int, out_hw
+ *   MOE_OUT: xn, shared_gate, experts, shared, x (x updated in place)
+ *   RMSNORM: x, w, y (eps_bits, plus_one of the descriptor)
  * `m` is the rows of the block (the kernels read state[3], never beyond m). */
 int hb_launch(hb_gpu *gpu, int32_t kernel, const hb_range *bindings, uint32_t nbind, uint32_t m);
 

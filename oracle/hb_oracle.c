@@ -17,6 +17,8 @@
  *   - hbo_rmsnorm_rows: closed forms (constant rows: x' = w exactly; one
  *     nonzero element), its two summation orders against each other, and
  *     an f64 restatement within one bf16 ulp;
+ *   - hbo_moe_out: closed forms (zero gate weights: g = bf16(sigmoid(0)) =
+ *     0.5; shared = 0: x + experts) and an f64 restatement;
  *   - hbo_route / hbo_moe_sort / hbo_combine / hbo_swiglu: brute-force
  *     restatements in numpy (argsort with ties, set invariants, tile cover),
  *     and hbo_expf against libm within 2 ulp over a dense sweep.
@@ -428,6 +430,48 @@ void hbo_rmsnorm_rows(const uint16_t *x, const uint16_t *w, int m, int k, float 
             float wf = hbo_bf16_to_f32(w[i]);
             if (plus_one) wf = wf + 1.0f;
             out[(size_t)j * k + i] = hbo_f32_to_bf16((hbo_bf16_to_f32(xr[i]) * inv) * wf);
+        }
+    }
+}
+
+/* qwen_kernels.rs:2163-2214 (moe_out): per row, g = bf16(sigmoid(bf16(gate .
+ * xn))), x = bf16(x + bf16(experts + bf16(g * shared))) in place.  order 0
+ * sums the dot as the HIP kernel does (256 threads' fma chains over t, t+256,
+ * ..., the 64-lane butterfly, the 4 waves in order); order 1 in increasing
+ * index.  The reference's own order is Apple's threadgroup reduction (parity
+ * with its bits unpinned). */
+void hbo_moe_out(const uint16_t *xn, const uint16_t *gate, const uint16_t *ex, const uint16_t *sh,
+                 uint16_t *x, int rows, int d, int order) {
+    for (int r = 0; r < rows; r++) {
+        const uint16_t *xr = xn + (size_t)r * d;
+        float dot = 0.0f;
+        if (order == 1) {
+            for (int i = 0; i < d; i++) dot = fmaf(hbo_bf16_to_f32(xr[i]), hbo_bf16_to_f32(gate[i]), dot);
+        } else {
+            float t[256], wave[4];
+            for (int th = 0; th < 256; th++) {
+                float a = 0.0f;
+                for (int i = th; i < d; i += 256) a = fmaf(hbo_bf16_to_f32(xr[i]), hbo_bf16_to_f32(gate[i]), a);
+                t[th] = a;
+            }
+            for (int wv = 0; wv < 4; wv++) {
+                float l[64];
+                memcpy(l, t + 64 * wv, sizeof l);
+                for (int s = 32; s >= 1; s >>= 1) {
+                    float nl[64];
+                    for (int i = 0; i < 64; i++) nl[i] = l[i] + l[i ^ s];
+                    memcpy(l, nl, sizeof l);
+                }
+                wave[wv] = l[0];
+            }
+            dot = ((wave[0] + wave[1]) + wave[2]) + wave[3];
+        }
+        float g = hbo_round_bf16(sigmoid(hbo_round_bf16(dot)));
+        for (int i = 0; i < d; i++) {
+            size_t at = (size_t)r * d + i;
+            float s = hbo_round_bf16(g * hbo_bf16_to_f32(sh[at]));
+            float o = hbo_round_bf16(hbo_bf16_to_f32(ex[at]) + s);
+            x[at] = hbo_f32_to_bf16(hbo_bf16_to_f32(x[at]) + o);
         }
     }
 }

@@ -164,6 +164,18 @@ def rmsnorm_rows(x, w, eps, plus_one=False, order=0):
     return out
 
 
+lib.hbo_moe_out.argtypes = [_P, _P, _P, _P, _P, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+
+
+def moe_out(xn, gate, ex, sh, x, order=0):
+    """moe_out (hb_oracle.c hbo_moe_out): the updated x (a copy)."""
+    xn, gate, ex, sh = (_c(a, np.uint16) for a in (xn, gate, ex, sh))
+    out = np.array(x, dtype=np.uint16, copy=True)
+    rows, d = out.shape
+    lib.hbo_moe_out(_p(xn), _p(gate), _p(ex), _p(sh), _p(out), rows, d, order)
+    return out
+
+
 def combine(y, route_, top_k, d):
     y = _c(y, np.uint16)
     route_ = _c(route_, np.uint32)

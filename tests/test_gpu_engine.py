@@ -164,3 +164,67 @@ def test_moe_layer_through_picked_kernels(gpu):
     layer.free()
     gpu.free(Wgu)
     gpu.free(Wdn)
+
+
+def test_rmsnorm_kernel_bit_exact(gpu):
+    """The block's input norm: the oracle restates the kernel's summation
+    order, so every output bit matches (rows of 2048 and of 2560)."""
+    for d, p1 in ((2048, True), (2560, False)):
+        x = hb.normal_bf16(51, 2.0, (37, d))
+        w = hb.normal_bf16(52, 0.1, (d,))
+        X, Wb, Y = gpu.alloc_with(x), gpu.alloc_with(w), gpu.alloc(37 * d * 2)
+        k = gpu.pipeline(hb.rmsnorm(d, 1e-6, p1))
+        gpu.launch(k, [hb.r(X), hb.r(Wb), hb.r(Y)], 37)
+        got = gpu.download(Y, np.uint16, 37 * d).reshape(37, d)
+        assert np.array_equal(got, orc.rmsnorm_rows(x, w, 1e-6, p1, 0)), d
+        for b in (X, Wb, Y):
+            gpu.free(b)
+
+
+def test_moe_block_through_picked_kernels(gpu):
+    """The whole sparse MLP of a qwen3_5_moe layer (qwen.rs:2691-2732) on the
+    picked kernels, each stage against the oracle from the GPU's own input to
+    it: the norm and the route bit for bit, the router GEMM and the shared
+    expert within the contract, the routed experts within the reference's
+    gate, and moe_out bit for bit."""
+    E, K_, H, MI, SI, rows = 64, 8, 512, 256, 256, 192
+    host = {"post_norm": hb.normal_bf16(61, 0.1, (H,)), "router": hb.normal_bf16(62, 0.05, (E, H)),
+            "w_gate_up": hb.normal_bf16(63, 0.02, (E * 2 * MI, H)),
+            "w_down": hb.normal_bf16(64, 0.02, (E * H, MI)),
+            "s_gate_up": hb.normal_bf16(65, 0.02, (2 * SI, H)), "s_down": hb.normal_bf16(66, 0.02, (H, SI)),
+            "shared_gate": hb.normal_bf16(67, 0.05, (H,))}
+    w = {nm: gpu.alloc_with(a) for nm, a in host.items()}
+    x0 = hb.normal_bf16(68, 1.0, (rows, H))
+    with hb.Engine(gpu, "") as e:
+        blk = hb.MoeBlock(gpu, e, E, K_, H, MI, SI, rows, w, x0)
+    try:
+        gpu.upload(blk.buf["x"], x0)
+        gpu.time_ops(blk.ops(), 1)
+        L = blk.layer.buf
+        dl = lambda b, n, t=np.uint16: gpu.download(b, t, n)  # noqa: E731
+        xn = dl(L["x"], rows * H).reshape(rows, H)
+        assert np.array_equal(xn, orc.rmsnorm_rows(x0, host["post_norm"], 1e-6, True, 0))
+        scores = dl(L["scores"], rows * E).reshape(rows, E)
+        check_close(scores, orc.gemm(xn, host["router"]), H, abs_products(xn, host["router"]), "router")
+        route = dl(L["route"], rows * 2 * K_, np.uint32).reshape(rows, -1)
+        assert np.array_equal(route, orc.route(scores, K_))
+        sh = dl(blk.buf["s_h"], rows * SI).reshape(rows, SI)
+        ap = abs_products(xn, host["s_gate_up"])
+        check_close(sh, orc.gemm_swiglu(xn, host["s_gate_up"], SI), H,
+                    np.maximum(ap[:, :SI], ap[:, SI:]) * 2, "shared gate_up", ulps=4.0)
+        sout = dl(blk.buf["sout"], rows * H).reshape(rows, H)
+        check_close(sout, orc.gemm(sh, host["s_down"]), SI, abs_products(sh, host["s_down"]), "shared down")
+        esum = dl(L["out"], rows * H).reshape(rows, H)
+        lst, tiles = orc.moe_sort(route, K_, E, blk.layer.bm)
+        gu = orc.experts_gemm(xn, host["w_gate_up"], lst, tiles, H, 2 * MI, 1, K_, rows * K_)
+        ey = orc.experts_gemm(orc.swiglu(gu, MI), host["w_down"], lst, tiles, MI, H, 2, K_, rows * K_)
+        want = orc.combine(ey, route, K_, H)
+        from parity import bf16_to_f32
+        err = np.abs(bf16_to_f32(esum).astype(np.float64) - bf16_to_f32(want))
+        assert err.max() <= np.abs(bf16_to_f32(want)).max() / 64
+        x1 = dl(blk.buf["x"], rows * H).reshape(rows, H)
+        assert np.array_equal(x1, orc.moe_out(xn, host["shared_gate"], esum, sout, x0))
+    finally:
+        blk.free()
+        for b in w.values():
+            gpu.free(b)

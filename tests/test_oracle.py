@@ -360,3 +360,31 @@ def test_rmsnorm_orders_and_f64_within_one_ulp():
         assert np.all(np.abs(g - ref) <= ulp * 1.0001)
     d = np.abs(bf16_to_f32(a).astype(np.float64) - bf16_to_f32(b))
     assert np.all(d <= 2.0 ** (np.floor(np.log2(np.maximum(np.abs(bf16_to_f32(a)), 2.0 ** -126))) - 7))
+
+
+# ---- moe_out (qwen_kernels.rs:2163-2214) ----------------------------------
+
+def test_moe_out_closed_forms():
+    """Zero gate weights: dot = 0, g = bf16(sigmoid(0)) = 0.5 exactly, so x'
+    = bf16(x + bf16(ex + bf16(sh / 2))); shared = 0: x' = bf16(x + ex) --
+    and an f64 restatement of the gate within one bf16 ulp."""
+    rows, d = 3, 512
+    xn = hb_normal(41, 1.0, (rows, d))
+    ex = hb_normal(42, 1.0, (rows, d))
+    sh = hb_normal(43, 1.0, (rows, d))
+    x = hb_normal(44, 1.0, (rows, d))
+    f = lambda a: bf16_to_f32(a).astype(np.float32)  # noqa: E731
+    r = lambda v: bf16_to_f32(np.array([_bf16(t) for t in np.ravel(v)], np.uint16)).reshape(np.shape(v))  # noqa: E731
+    got = orc.moe_out(xn, np.zeros(d, np.uint16), ex, sh, x)
+    want = r(f(x) + r(f(ex) + r(np.float32(0.5) * f(sh))))
+    assert np.array_equal(bf16_to_f32(got), want.astype(np.float32))
+    got = orc.moe_out(xn, hb_normal(45, 0.05, d), ex, np.zeros((rows, d), np.uint16), x)
+    assert np.array_equal(bf16_to_f32(got), r(f(x) + f(ex)).astype(np.float32))
+    gate = hb_normal(46, 0.05, d)
+    for order in (0, 1):
+        got = orc.moe_out(xn, gate, np.zeros((rows, d), np.uint16), sh, np.zeros((rows, d), np.uint16), order)
+        dot = bf16_to_f32(xn).astype(np.float64) @ bf16_to_f32(gate).astype(np.float64)
+        g64 = 1.0 / (1.0 + np.exp(-dot))
+        ref = g64[:, None] * bf16_to_f32(sh).astype(np.float64)
+        ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -126))) - 7)
+        assert np.all(np.abs(bf16_to_f32(got) - ref) <= 3 * ulp)
