@@ -986,4 +986,20 @@ int hb_engine_experts(hb_engine* e, uint32_t experts, uint32_t top_k, uint32_t h
     return HB_OK;
 }
 
+uint32_t hb_blocks_of(uint32_t n, uint32_t chunk, uint32_t* starts, uint32_t* rows, uint32_t cap) {
+    if (!n) return 0;
+    const uint32_t c = chunk ? chunk : 1;
+    const uint32_t k = (n + c - 1) / c;
+    uint32_t size = (n + k - 1) / k;
+    size = (size + 63) / 64 * 64;
+    if (size > c) size = c;
+    uint32_t count = 0;
+    for (uint32_t at = 0; at < n; at += size, count++)
+        if (count < cap) {
+            starts[count] = at;
+            rows[count] = size < n - at ? size : n - at;
+        }
+    return count;
+}
+
 }  // extern "C"

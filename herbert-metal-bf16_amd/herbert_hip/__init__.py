@@ -636,3 +636,143 @@ class MoeBlock:
         self.layer.free()
         for buf in self.buf.values():
             self.gpu.free(buf)
+
+
+# ---- the checkpoint (model/qwen.rs:155-375) and the prefill block loop ----
+
+lib.hb_ckpt_open.argtypes = [ctypes.c_char_p, ctypes.POINTER(_P)]
+lib.hb_ckpt_close.argtypes = [_P]
+lib.hb_ckpt_close.restype = None
+lib.hb_ckpt_skipped.argtypes = [_P]
+lib.hb_ckpt_skipped.restype = ctypes.c_char_p
+lib.hb_ckpt_elements.argtypes = [_P, ctypes.c_char_p]
+lib.hb_ckpt_elements.restype = _u64
+lib.hb_ckpt_read.argtypes = [_P, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_u64), _u32, _P, _u64]
+lib.hb_ckpt_upload.argtypes = [_P, _P, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_u64), _u32,
+                               ctypes.POINTER(_u32)]
+lib.hb_blocks_of.argtypes = [_u32, _u32, ctypes.POINTER(_u32), ctypes.POINTER(_u32), _u32]
+lib.hb_blocks_of.restype = _u32
+
+
+class Checkpoint:
+    """Checkpoint (model/qwen.rs:155-375): the shards of `model_dir` mapped,
+    names normalised to the engine's keys ("N.field"), tensors read as bf16."""
+
+    def __init__(self, model_dir):
+        h = _P()
+        check(lib.hb_ckpt_open(os.fsencode(model_dir), ctypes.byref(h)))
+        self.h = h
+
+    def close(self):
+        if self.h:
+            lib.hb_ckpt_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def skipped(self):
+        return lib.hb_ckpt_skipped(self.h).decode()
+
+    def elements(self, key):
+        return lib.hb_ckpt_elements(self.h, key.encode())
+
+    def has(self, key):
+        return self.elements(key) > 0
+
+    @staticmethod
+    def _parts(parts):
+        keys = (ctypes.c_char_p * len(parts))(*[k.encode() for k, _ in parts])
+        lens = (_u64 * len(parts))(*[int(n) for _, n in parts])
+        return keys, lens
+
+    def read(self, parts):
+        """read_bf16_into: the (key, elements) parts one after the other, bf16."""
+        keys, lens = self._parts(parts)
+        total = sum(int(n) for _, n in parts)
+        out = np.empty(total, np.uint16)
+        check(lib.hb_ckpt_read(self.h, keys, lens, len(parts), out.ctypes.data_as(_P), total))
+        return out
+
+    def upload(self, gpu, parts):
+        """upload(&mut gpu, &ck, parts): the parts stacked in one new buffer."""
+        keys, lens = self._parts(parts)
+        b = _u32()
+        check(lib.hb_ckpt_upload(gpu.h, self.h, keys, lens, len(parts), ctypes.byref(b)))
+        gpu._sizes[b.value] = 2 * sum(int(n) for _, n in parts)
+        return b.value
+
+
+def blocks_of(n, chunk):
+    """blocks_of (qwen.rs:3017-3027): [(start, rows)] of a prompt of n rows."""
+    cap = n // 64 + 2
+    st, rw = (_u32 * cap)(), (_u32 * cap)()
+    c = lib.hb_blocks_of(int(n), int(chunk), st, rw, cap)
+    return [(st[i], rw[i]) for i in range(min(c, cap))]
+
+
+class PrefillMlp:
+    """The dense MLP half of a qwen layer's prefill (block_in, qwen.rs:2691-
+    2697 without the MoE): x -> post norm -> [gate | up] GEMM (+ SwiGLU, or
+    the fused kernel, gate_up_pipes) -> down GEMM added to x (Out::Residual),
+    over a prompt cut into blocks (blocks_of) with each block on the kernels
+    picked for its bucket (the smallest of the prefill buckets, qwen.rs:
+    1051-1063, holding its rows).  Weights from the checkpoint in the fused
+    layout the GEMMs read (qwen.rs:790-794)."""
+
+    def __init__(self, gpu, engine, ckpt, layer, hidden, inter, eps=1e-6, plus_one=True):
+        self.gpu, self.h, self.inter = gpu, hidden, inter
+        p = lambda f: "%d.%s" % (layer, f)  # noqa: E731
+        mlp = "mlp.shared_expert" if ckpt.has(p("mlp.shared_expert.gate_proj.weight")) else "mlp"
+        self.w = {"post_norm": ckpt.upload(gpu, [(p("post_attention_layernorm.weight"), hidden)]),
+                  "gate_up": ckpt.upload(gpu, [(p(mlp + ".gate_proj.weight"), inter * hidden),
+                                               (p(mlp + ".up_proj.weight"), inter * hidden)]),
+                  "down": ckpt.upload(gpu, [(p(mlp + ".down_proj.weight"), hidden * inter)])}
+        self.buckets = engine.buckets()
+        self.chunk = self.buckets[-1]
+        B = self.chunk
+        g = gpu
+        self.buf = {"xn": g.alloc(B * hidden * 2), "gu": g.alloc(B * 2 * inter * 2),
+                    "hh": g.alloc(B * inter * 2), "x": g.alloc(B * hidden * 2)}
+        self.norm_k = g.pipeline(rmsnorm(hidden, eps, plus_one))
+        self.kern = {}
+        for m in self.buckets:
+            st = g.alloc_with(np.array([0, 0, 0, m], np.uint32))
+            b, w = self.buf, self.w
+            gu_k, sw_k = engine.gate_up(hidden, inter, r(st), r(w["gate_up"]), r(b["xn"]), r(b["gu"]),
+                                        r(b["hh"]), m)
+            dn_k = engine.gemm(inter, hidden, Out.Residual, r(st), r(w["down"]), r(b["hh"]), r(b["x"]), m)
+            self.kern[m] = (gu_k, sw_k, dn_k)
+            g.free(st)
+
+    def ops(self, x, n, states):
+        """The ops of a prompt of n rows of the residual stream `x` (a buffer
+        of [n][hidden] bf16, updated in place); `states`: one state buffer per
+        block (blocks_of(n, chunk)), state[3] its rows."""
+        h, b, w = self.h, self.buf, self.w
+        ops = []
+        for (start, rows), st in zip(blocks_of(n, self.chunk), states):
+            m = min(bk for bk in self.buckets if bk >= rows)
+            gu_k, sw_k, dn_k = self.kern[m]
+            xr = r(x, start * h * 2, rows * h * 2)
+            s = r(st)
+            ops.append(Op(self.norm_k, [xr, r(w["post_norm"]), r(b["xn"])], rows))
+            if sw_k >= 0:
+                ops.append(Op(gu_k, [s, r(w["gate_up"]), r(b["xn"]), r(b["gu"]), s, s], rows))
+                ops.append(Op(sw_k, [r(b["gu"]), r(b["hh"])], rows))
+            else:
+                ops.append(Op(gu_k, [s, r(w["gate_up"]), r(b["xn"]), r(b["hh"]), s, s], rows))
+            ops.append(Op(dn_k, [s, r(w["down"]), r(b["hh"]), xr, s, s], rows))
+        return ops
+
+    def states(self, n):
+        """One state buffer per block of a prompt of n rows (free them after)."""
+        return [self.gpu.alloc_with(np.array([0, 0, 0, rows], np.uint32))
+                for _, rows in blocks_of(n, self.chunk)]
+
+    def free(self):
+        for buf in list(self.buf.values()) + list(self.w.values()):
+            self.gpu.free(buf)

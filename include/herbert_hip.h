@@ -290,6 +290,36 @@ int hb_engine_log_summary(hb_engine *engine);
  * ones (the way check_candidates meets a kernel that builds but computes
  * something else, qwen.rs:2488-2496: it must be logged wrong, never picked). */
 int hb_engine_add_gemm_candidate(hb_engine *engine, const char *name, const hb_desc *desc);
+/* ---- the checkpoint (model/qwen.rs:155-375) ---------------------------
+ * Checkpoint::load: `dir` holds model.safetensors.index.json (its shards)
+ * or model.safetensors; the shards are mapped read-only and every tensor
+ * name normalised to the engine's key (model/qwen.rs:102-153: "N.field" for
+ * "model.language_model.layers.N.field" and the other Hugging Face
+ * prefixes; "embed_tokens", "norm", "lm_head"), the fields of the matmul
+ * path and its norms kept, the others counted in hb_ckpt_skipped (the
+ * reference's "[loader] skipped" line).  BF16, F16 and F32 tensors; each
+ * element rounded once to bf16 when read (bf16_at, :92-99). */
+typedef struct hb_ckpt hb_ckpt;
+int hb_ckpt_open(const char *dir, hb_ckpt **ckpt);
+void hb_ckpt_close(hb_ckpt *ckpt);
+const char *hb_ckpt_skipped(hb_ckpt *ckpt);
+/* The key's element count, 0 when the checkpoint has no such tensor. */
+uint64_t hb_ckpt_elements(hb_ckpt *ckpt, const char *key);
+/* read_bf16_into (model/qwen.rs:338-361): the tensors `keys`, each checked
+ * against `lens` elements, one after the other into dst (bf16). */
+int hb_ckpt_read(hb_ckpt *ckpt, const char *const *keys, const uint64_t *lens, uint32_t n,
+                 uint16_t *dst, uint64_t dst_elements);
+/* QwenEngine's upload(&mut gpu, &ck, &[(key, len), ...]) (qwen.rs:776-835):
+ * the same parts stacked into one new buffer, e.g. [q | k | v] or
+ * [gate | up] rows, the fused layouts the GEMMs read. */
+int hb_ckpt_upload(hb_gpu *gpu, hb_ckpt *ckpt, const char *const *keys, const uint64_t *lens,
+                   uint32_t n, hb_buf *out);
+
+/* blocks_of (qwen.rs:3017-3027): a prompt of n rows cut into ceil(n / chunk)
+ * blocks of equal size rounded up to 64 rows (the last shorter); starts and
+ * rows of up to `cap` blocks; returns the count. */
+uint32_t hb_blocks_of(uint32_t n, uint32_t chunk, uint32_t *starts, uint32_t *rows, uint32_t cap);
+
 /* Tune::default + Tune::apply + Tune::summary without a device: HB_OK and
  * the summary in `summary` (cap bytes), or HB_ERR_INVALID and the
  * reference's message in hb_last_error(). */

@@ -228,3 +228,48 @@ def test_moe_block_through_picked_kernels(gpu):
         blk.free()
         for b in w.values():
             gpu.free(b)
+
+
+def test_prefill_mlp_from_checkpoint_in_blocks(gpu, tmp_path):
+    """The dense MLP half of a layer's prefill over a 300-row prompt cut into
+    blocks of prefill.block=128 (blocks_of: 128, 128, 44 rows, on the picks of
+    buckets 128 and 64), weights read from a two-shard checkpoint in the
+    Hugging Face layout and stacked [gate | up]: every row within the contract
+    of the oracle's norm -> GEMM -> SwiGLU -> GEMM (Residual) chain."""
+    from st_writer import write_model
+    h, inter, n = 512, 768, 300
+    gate = hb.normal_bf16(71, 0.02, (inter, h))
+    up = hb.normal_bf16(72, 0.02, (inter, h))
+    down = hb.normal_bf16(73, 0.02, (h, inter))
+    pn = hb.normal_bf16(74, 0.1, (h,))
+    write_model(str(tmp_path / "m"), [
+        {"model.language_model.layers.3.mlp.gate_proj.weight": ("BF16", gate),
+         "model.language_model.layers.3.post_attention_layernorm.weight": ("BF16", pn)},
+        {"model.language_model.layers.3.mlp.up_proj.weight": ("BF16", up),
+         "model.language_model.layers.3.mlp.down_proj.weight": ("BF16", down)}])
+    x0 = hb.normal_bf16(75, 1.0, (n, h))
+    with hb.Checkpoint(str(tmp_path / "m")) as ck, hb.Engine(gpu, "prefill.block=128") as e:
+        mlp = hb.PrefillMlp(gpu, e, ck, 3, h, inter)
+        log = e.log()
+    assert mlp.buckets == [64, 128], mlp.buckets
+    assert "512x1536, 64 rows" in log and "512x1536, 128 rows" in log, log
+    X = gpu.alloc_with(x0)
+    states = mlp.states(n)
+    try:
+        gpu.time_ops(mlp.ops(X, n, states), 1)
+        got = gpu.download(X, np.uint16, n * h).reshape(n, h)
+        xn = orc.rmsnorm_rows(x0, pn, 1e-6, True, 0)
+        w_gu = np.concatenate([gate, up])
+        hh = orc.gemm_swiglu(xn, w_gu, inter)
+        want = orc.gemm(hh, down, orc.OUT_RESIDUAL, x0)
+        # Each stage's rounding (the SwiGLU's inputs within 2 ulp) joins the
+        # down GEMM's: the bound of the h values' ulps through |W_down|.
+        from parity import bf16_to_f32, bf16_ulp
+        hf = np.abs(bf16_to_f32(hh).astype(np.float64))
+        extra = 4 * bf16_ulp(hf) @ np.abs(bf16_to_f32(down).astype(np.float64)).T
+        check_close(got, want, inter, abs_products(hh, down) + extra, "prefill mlp", ulps=3.0,
+                    acc=orc.gemm(hh, down, orc.OUT_F32))
+    finally:
+        for b in states + [X]:
+            gpu.free(b)
+        mlp.free()
