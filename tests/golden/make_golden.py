@@ -121,6 +121,38 @@ def main():
             assert abs(float(e) - math.exp(float(v))) <= 2 * ulp, v
     g["exp_in"], g["exp_out"] = xe, ye
 
+    # XSrc::Norm / rmsnorm: rows of 512 (the kernel's summation order, eps
+    # 1e-6, plus_one); row 0 constant 2 with eps 0 would give w + 1 exactly --
+    # here with eps each row is within one bf16 ulp of an f64 restatement.
+    nx = rne_branchy((rng.standard_normal((3, 512)) * 3).astype(np.float32).view(np.uint32))
+    nx[0] = 0x4000  # 2.0 everywhere
+    nw = rne_branchy((rng.standard_normal(512) * 0.1).astype(np.float32).view(np.uint32))
+    ny = orc.rmsnorm_rows(nx, nw, 1e-6, True, 0)
+    xf = f32(nx).astype(np.float64)
+    ref = xf / np.sqrt((xf * xf).mean(axis=1, keepdims=True) + 1e-6) * (f32(nw).astype(np.float64) + 1)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -126))) - 7)
+    assert np.all(np.abs(f32(ny) - ref) <= ulp)
+    assert np.array_equal(orc.rmsnorm_rows(nx[:1], nw, 0.0, True, 0)[0],
+                          rne_branchy((f32(nw) + np.float32(1)).view(np.uint32)))
+    g["nx"], g["nw"], g["ny"] = nx, nw, ny
+
+    # moe_out: rows of 512; with zero gate weights g = 0.5 exactly (closed
+    # form checked), and random gate weights checked against f64 within 3 ulp.
+    ox = rne_branchy(rng.standard_normal((3, 512)).astype(np.float32).view(np.uint32))
+    oe = rne_branchy(rng.standard_normal((3, 512)).astype(np.float32).view(np.uint32))
+    osh = rne_branchy(rng.standard_normal((3, 512)).astype(np.float32).view(np.uint32))
+    ox0 = rne_branchy(rng.standard_normal((3, 512)).astype(np.float32).view(np.uint32))
+    og = rne_branchy((rng.standard_normal(512) * 0.05).astype(np.float32).view(np.uint32))
+    rb = lambda v: f32(rne_branchy(np.asarray(v, np.float32).view(np.uint32)))  # noqa: E731
+    zero = orc.moe_out(ox, np.zeros(512, np.uint16), oe, osh, ox0)
+    assert np.array_equal(f32(zero), rb(f32(ox0) + rb(f32(oe) + rb(np.float32(0.5) * f32(osh)))))
+    oy = orc.moe_out(ox, og, oe, osh, ox0)
+    gate = 1 / (1 + np.exp(-(f32(ox).astype(np.float64) @ f32(og).astype(np.float64))))
+    ref = f32(ox0) + f32(oe) + gate[:, None] * f32(osh)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -126))) - 7)
+    assert np.all(np.abs(f32(oy) - ref) <= 3 * ulp + 2 ** -8 * (np.abs(f32(oe)) + np.abs(f32(osh))))
+    g["ox"], g["og"], g["oe"], g["os"], g["ox0"], g["oy"] = ox, og, oe, osh, ox0, oy
+
     path = os.path.join(HERE, "golden.npz")
     np.savez_compressed(path, **g)
     print("wrote %s (%d bytes, %d arrays)" % (path, os.path.getsize(path), len(g)))

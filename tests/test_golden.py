@@ -37,3 +37,8 @@ def test_golden_moe():
 def test_golden_expf():
     got = np.array([orc.expf(float(v)) for v in G["exp_in"]], np.float32)
     assert np.array_equal(got.view(np.uint32), G["exp_out"].view(np.uint32))
+
+
+def test_golden_rmsnorm_and_moe_out():
+    assert np.array_equal(orc.rmsnorm_rows(G["nx"], G["nw"], 1e-6, True, 0), G["ny"])
+    assert np.array_equal(orc.moe_out(G["ox"], G["og"], G["oe"], G["os"], G["ox0"]), G["oy"])

@@ -91,3 +91,14 @@ def _run_h(gpu, desc, x, w):
     finally:
         for b in (st, W, X, H):
             gpu.free(b)
+
+
+def test_golden_rmsnorm_and_moe_out_kernels(gpu):
+    """The block's norm and moe_out kernels on the fixtures, bit for bit
+    (the oracle restates their reduction order)."""
+    res = launch(gpu, hb.rmsnorm(512, 1e-6, True), [G["nx"], G["nw"], 3 * 512 * 2], 3,
+                 {2: (np.uint16, 3 * 512)})
+    assert np.array_equal(res[2].reshape(3, 512), G["ny"])
+    res = launch(gpu, hb.moe_out(512), [G["ox"], G["og"], G["oe"], G["os"], G["ox0"]], 3,
+                 {4: (np.uint16, 3 * 512)})
+    assert np.array_equal(res[4].reshape(3, 512), G["oy"])
