@@ -9,6 +9,7 @@
 #include <cctype>
 #include <cstdlib>
 #include <cstdio>
+#include <cstring>
 
 #include "hb_internal.h"
 
@@ -170,6 +171,9 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
                 return fail(HB_ERR_UNSUPPORTED, "matvec Out::Swiglu: even rows (gate and up) and n");
             if (d.xsrc == HB_XSRC_NORM && ((uint64_t)d.mv_m * d.k * 2 > 65536 || d.k % 256))
                 return fail(HB_ERR_UNSUPPORTED, "matvec XSrc::Norm: m*k*2 <= 64 KiB of LDS, k a multiple of 256");
+            if (d.x_lds > 1 || (d.x_lds && (d.form == 1 || (uint64_t)d.mv_m * d.k * 2 > 65536)))
+                return fail(HB_ERR_UNSUPPORTED, "matvec x_lds: VALU forms, m*k*2 <= 64 KiB of LDS");
+            const bool xl = d.x_lds && d.xsrc != HB_XSRC_NORM;
             if (!d.k || !d.n || d.k % (8 * d.split) || (d.split != 1 && d.split != 2 && d.split != 4))
                 return fail(HB_ERR_UNSUPPORTED, "matvec: K a multiple of 8*split, split 1, 2 or 4");
             if (d.form != 1 && (d.rows > 8 || !d.rows || d.rows * d.mv_m > 64 || d.mv_m > 16))
@@ -182,6 +186,7 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
             if (d.xsrc == HB_XSRC_SWIGLU) snprintf(xtag, sizeof xtag, "_swi");
             if (d.xsrc == HB_XSRC_NORM)
                 snprintf(xtag, sizeof xtag, "_nrm%08x%s", d.eps_bits, d.plus_one ? "p1" : "");
+            if (xl) strncat(xtag, "_xl", sizeof xtag - strlen(xtag) - 1);
             snprintf(name, sizeof name, "matvec_%ux%u%s%s_r%u_k%u%s_m%u_%s_u%u", d.k, d.n, xtag,
                      d.out == HB_OUT_F32 ? "_f32" : d.out == HB_OUT_RESIDUAL ? "_res"
                                                   : d.out == HB_OUT_SWIGLU ? "_sw" : "",
@@ -194,7 +199,8 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
             e->defines = {D("HB_K", d.k),         D("HB_N", d.n),          D("HB_OUT", d.out),
                           D("HB_MV_M", d.mv_m),   D("HB_FORM", d.form),    D("HB_ROWS", d.rows),
                           D("HB_SPLIT", d.split), D("HB_PERSIST", d.persist), D("HB_UNROLL", d.unroll),
-                          D("HB_XSRC", d.xsrc),   D("HB_EPS", d.eps_bits), D("HB_PLUS1", d.plus_one)};
+                          D("HB_XSRC", d.xsrc),   D("HB_EPS", d.eps_bits), D("HB_PLUS1", d.plus_one),
+                          D("HB_XLDS", xl ? 1 : 0)};
             return HB_OK;
         }
         case HB_KIND_ROUTE:

@@ -825,6 +825,20 @@ int hb_engine_matvec_fused(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, u
                     add((mv_m > 1 ? "d" : "r") + std::to_string(rows) + tag + "u8", d8);
                 }
             }
+    // The x rows staged in LDS once per workgroup (plain or XSrc::Swiglu,
+    // m*K*2 <= 64 KiB): for several rows, where reloading x per row block
+    // through the vector memory path costs more than the W stream, and for
+    // XSrc::Swiglu, whose SwiGLU is then computed once per workgroup.
+    // Persistent workgroups (two and four per CU) stage it fewer times.
+    if ((mv_m > 1 || xsrc == HB_XSRC_SWIGLU) && xsrc != HB_XSRC_NORM && (uint64_t)mv_m * k * 2 <= 65536)
+        for (uint32_t p : {0u, 512u, 1024u})
+            for (uint32_t rows : {1u, 2u, 4u}) {
+                if (rows * mv_m > 64 || (out == HB_OUT_SWIGLU && rows < 2)) continue;
+                hb_desc dx = desc(mv_m > 1 ? 2 : 0, rows, 1, p);
+                dx.unroll = 8;
+                dx.x_lds = 1;
+                add((mv_m > 1 ? "d" : "r") + std::to_string(rows) + (p ? "p" + std::to_string(p) : "") + "u8xl", dx);
+            }
     for (uint32_t split : splits)
         for (uint32_t p : pers) {
             if (fused) break;  // the fusions are VALU forms

@@ -57,6 +57,15 @@ constexpr u32 RB = 16;
 #ifndef HB_XSRC
 #define HB_XSRC 0
 #endif
+#ifndef HB_PROBE_NOX
+#define HB_PROBE_NOX 0
+#endif
+#ifndef HB_XLDS
+#define HB_XLDS 0
+#endif
+// x rows in LDS: XSrc::Norm's normed rows, or (HB_XLDS) the plain or
+// swiglu'd rows staged once per workgroup.
+#define HB_XIN_LDS (HB_XSRC == 2 || HB_XLDS)
 #ifndef HB_EPS
 #define HB_EPS 0
 #endif
@@ -73,6 +82,7 @@ constexpr u32 NBLK = (NOUT + RO - 1) / RO;
 constexpr u32 KS = K / SPLIT;                 // K of one wave's range
 static_assert(!SWO || (RB % 2 == 0 && N % 2 == 0 && HB_FORM != 1), "Out::Swiglu: VALU forms, even rows");
 static_assert(HB_XSRC == 0 || HB_FORM != 1, "XSrc fusions: VALU forms");
+static_assert(!HB_XIN_LDS || (HB_FORM != 1 && MV * K * 2 <= 65536), "x in LDS: VALU forms, m*K*2 <= 64 KiB");
 
 static_assert(WAVES % SPLIT == 0, "split divides the waves");
 static_assert(K % (8 * SPLIT) == 0 && KS % 8 == 0, "K split in whole chunks");
@@ -116,14 +126,16 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
     const u32 wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const u32 gi = wave / SPLIT, sp = wave % SPLIT;  // row block in the group, K part
     const u32 m = m_launch < MV ? m_launch : MV;
+#if HB_XIN_LDS
+    __shared__ u32x4 xn4[MV * K / 8];
+#endif
 #if HB_XSRC == 2
     // XSrc::Norm (kernels.rs:355-440, rmsnorm :48-103): each x row's RMSNorm
     // into LDS as bf16 before the matvec.  ss = sum of x^2: thread t's fma
     // chain over elements t, t+256, ..., the 64 lanes' butterfly, then the 4
     // waves' sums in wave order; m = ss * (1/K) + eps; inv = 1/sqrt(m)
     // (correctly rounded); x' = bf16((x * inv) * w) with w + 1 for plus_one.
-    static_assert(K % 256 == 0 && MV * K * 2 <= 65536, "XSrc::Norm: K a multiple of 256, m*K*2 <= 64 KiB");
-    __shared__ u32x4 xn4[MV * K / 8];
+    static_assert(K % 256 == 0, "XSrc::Norm: K a multiple of 256");
     __shared__ float nred[WAVES * MV];
     {
         constexpr u32 PER = K / 256;
@@ -159,11 +171,9 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
         __syncthreads();
     }
 #endif
-    // 8 bf16 of x row jj at element `off` (XSrc: plain, swiglu'd, normed).
-    auto xload = [&](u32 jj, u32 off) HB_INLINE2 -> u32x4 {
-#if HB_XSRC == 2
-        return xn4[(jj * K + off) / 8];
-#elif HB_XSRC == 1
+    // 8 bf16 of x row jj at element `off` from memory (XSrc: plain, swiglu'd).
+    auto xmem = [&](u32 jj, u32 off) HB_INLINE2 -> u32x4 {
+#if HB_XSRC == 1
         const u32x4 g = *(const u32x4*)(x + (u64)jj * 2 * K + off);
         const u32x4 u = *(const u32x4*)(x + (u64)jj * 2 * K + K + off);
         u32x4 h;
@@ -173,6 +183,22 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
         return h;
 #else
         return *(const u32x4*)(x + (u64)jj * K + off);
+#endif
+    };
+#if HB_XLDS && HB_XSRC != 2
+    // Every x row's 16-byte chunks into LDS once (rows past m repeat row
+    // m-1, as the loads below would).
+    for (u32 c = tid; c < MV * K / 8; c += NT) {
+        const u32 j = c / (K / 8), jj = j < m ? j : m - 1;
+        xn4[c] = xmem(jj, (c % (K / 8)) * 8);
+    }
+    __syncthreads();
+#endif
+    auto xload = [&](u32 jj, u32 off) HB_INLINE2 -> u32x4 {
+#if HB_XIN_LDS
+        return xn4[(jj * K + off) / 8];
+#else
+        return xmem(jj, off);
 #endif
     };
     const u32 k0 = sp * KS;
@@ -227,7 +253,13 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
 #pragma unroll
                 for (u32 j = 0; j < MV; j++) {
                     const u32 jj = j < m ? j : m - 1;
+#if HB_PROBE_NOX
+                    // Kernel development only (wrong results): no x loads, W stands in.
+                    xs[j] = wv[u][j % RB];
+                    (void)jj;
+#else
                     xs[j] = on ? xload(jj, k0 + (c0 + 64 * u) * 8) : u32x4{0u, 0u, 0u, 0u};
+#endif
                 }
 #pragma unroll
                 for (u32 j = 0; j < MV; j++) {

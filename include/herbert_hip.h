@@ -146,7 +146,11 @@ typedef struct hb_desc {
     /* matvec: enum hb_xsrc; XSrc::Norm's epsilon (the f32's bits) and
      * plus_one (weights used as w + 1). */
     uint32_t xsrc, eps_bits, plus_one;
-    uint32_t reserved[2];
+    /* matvec (VALU forms): 1 = the x rows (plain, or XSrc::Swiglu's h) are
+     * staged once per workgroup into LDS (m*k*2 <= 64 KiB) and every row
+     * block reads them from there; XSrc::Norm always does. */
+    uint32_t x_lds;
+    uint32_t reserved;
 } hb_desc;
 
 /* Gpu::pipeline(&Emitted) (metal/gpu.rs:127-148) for the kernel the

@@ -183,3 +183,50 @@ def test_matvec_out_swiglu(gpu, form, m):
     assert np.array_equal(got, want_bits), "Out::Swiglu != swiglu of the rounded sums"
     check_close(got, orc.gemm_swiglu(x, w, nf), k,
                 np.maximum(ap[:, :nf], ap[:, nf:]) * 2, "out swiglu %s m=%d" % (form, m), ulps=4.0)
+
+
+XL_FORMS = {"dot2_r2_u8_xl_p512": dict(form=2, rows=2, split=1, unroll=8, persist=512),
+            "valu_r4_xl": dict(form=0, rows=4, split=1),
+            "dot2_r1_u8_xl_p1024": dict(form=2, rows=1, split=1, unroll=8, persist=1024)}
+
+
+@pytest.mark.parametrize("m", [1, 3, 8])
+@pytest.mark.parametrize("form", sorted(XL_FORMS))
+@pytest.mark.parametrize("name,k,n,out", SHAPES[:3])
+def test_matvec_x_in_lds(gpu, name, k, n, out, form, m):
+    """x staged in LDS once per workgroup: bit-equal to the same form reading
+    x from memory (the same sums in the same order), and within the contract
+    of the oracle; m=3 on a kernel built for 8 rows."""
+    x = hb.normal_bf16(0x5EED0023, 1.0, (m, k))
+    w = hb.normal_bf16(0x5EED0024, 0.02, (n, k))
+    y0 = hb.normal_bf16(19, 1.0, (m, n)) if out == 2 else None
+    got = run_mv(gpu, x, w, out, y0, x_lds=True, **XL_FORMS[form])
+    ref = run_mv(gpu, x, w, out, y0, **XL_FORMS[form])
+    assert np.array_equal(got, ref), "%s %s m=%d: x in LDS differs from x from memory" % (name, form, m)
+    want = orc.gemm(x, w, out, y0)
+    acc = orc.gemm(x, w, orc.OUT_F32) if out == 2 else None
+    check_close(got, want, k, abs_products(x, w), "%s %s xl m=%d" % (name, form, m), acc=acc)
+
+
+@pytest.mark.parametrize("m", [1, 2])
+def test_matvec_x_in_lds_fusions(gpu, m):
+    """XSrc::Swiglu with the swiglu'd x staged in LDS (down, K=9216, built for
+    2 rows: 36 KiB), and Out::Swiglu with x in LDS: bit-equal to the forms
+    reading x from memory."""
+    k, n = 9216, 2560
+    gu = hb.normal_bf16(0x5EED0025, 1.0, (m, 2 * k))
+    w = hb.normal_bf16(0x5EED0026, 0.02, (n, k))
+    y0 = hb.normal_bf16(21, 1.0, (m, n))
+    f = dict(form=2 if m > 1 else 0, rows=2, split=1, unroll=8, persist=512)
+    got = run_mv_fused(gpu, gu, w, hb.Out.Residual, y0, 2, xsrc=hb.XSrc.Swiglu, x_lds=True, **f)
+    ref = run_mv_fused(gpu, gu, w, hb.Out.Residual, y0, 2, xsrc=hb.XSrc.Swiglu, **f)
+    assert np.array_equal(got, ref), "XSrc::Swiglu: x in LDS differs from x from memory"
+    xs = orc.swiglu(gu, k)
+    check_close(got, orc.gemm(xs, w, orc.OUT_RESIDUAL, y0), k, abs_products(xs, w),
+                "swiglu x xl m=%d" % m, acc=orc.gemm(xs, w, orc.OUT_F32))
+    k2, nf = 2560, 9216
+    x = hb.normal_bf16(0x5EED0027, 1.0, (m, k2))
+    w2 = hb.normal_bf16(0x5EED0028, 0.02, (2 * nf, k2))
+    got = run_mv_fused(gpu, x, w2, hb.Out.Swiglu, None, 2, x_lds=True, **f)
+    ref = run_mv_fused(gpu, x, w2, hb.Out.Swiglu, None, 2, **f)
+    assert np.array_equal(got, ref), "Out::Swiglu: x in LDS differs from x from memory"
