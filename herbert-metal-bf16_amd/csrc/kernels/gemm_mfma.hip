@@ -70,6 +70,7 @@ constexpr u32 KT = K / BK;
 #ifndef HB_BAND
 #define HB_BAND 0
 #endif
+
 constexpr bool SWI = HB_SWIGLU != 0;
 constexpr u32 BF = SWI ? BN / 2 : BN;       // output columns of a tile
 constexpr u32 NTILES = (N + BF - 1) / BF;
@@ -247,6 +248,10 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
         const u32 p = tid + q * NT, r = p / CH;
         const u32 cc = HB_DMA ? ((p % CH) ^ ((r >> HB_SWZ) & (CH - 1))) : p % CH;
         xoff[q] = x_row(r) * K + cc * 8;
+        // Direct-to-LDS: rows past the tile's (never stored) at a byte
+        // offset past the buffer resource's range (0x7fffffff bytes), so
+        // the load writes zeros to LDS without a memory access.
+        if (HB_DMA && r >= rows) xoff[q] = 0x40000000u;
     }
 #pragma unroll
     for (u32 q = 0; q < W_LD; q++) {
