@@ -98,7 +98,9 @@ HB_DEV u32 lpos(u32 r, u32 c) { return r * CH + (c ^ ((r >> HB_SWZ) & (CH - 1)))
 
 // HB_PROBE_SKIP (kernel development only; wrong results): bit 0 drops the
 // global loads, bit 1 the MFMAs (their operands kept live), bit 2 the LDS
-// fragment reads (the registers kept, opaque) -- to time each part alone.
+// fragment reads (the registers kept, opaque), bit 3 sends every global load
+// past the buffer's range (the load instructions kept, no memory access) --
+// to time each part alone.
 #ifndef HB_PROBE_SKIP
 #define HB_PROBE_SKIP 0
 #endif
@@ -252,12 +254,14 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
         // offset past the buffer resource's range (0x7fffffff bytes), so
         // the load writes zeros to LDS without a memory access.
         if (HB_DMA && r >= rows) xoff[q] = 0x40000000u;
+        if (HB_PROBE_SKIP & 8) xoff[q] = 0x40000000u;
     }
 #pragma unroll
     for (u32 q = 0; q < W_LD; q++) {
         const u32 p = tid + q * NT, r = p / CH;
         const u32 cc = HB_DMA ? ((p % CH) ^ ((r >> HB_SWZ) & (CH - 1))) : p % CH;
         woff[q] = w_row(r) * K + cc * 8;
+        if (HB_PROBE_SKIP & 8) woff[q] = 0x40000000u;
     }
 
     acc_t acc[IN][IM];
