@@ -383,6 +383,14 @@ int check_bindings(const hb_desc& d, const uint64_t* s, uint32_t nbind, uint32_t
             if (d.rows_max && m > d.rows_max)
                 return fail(HB_ERR_INVALID, "m beyond the kernel's rows_max");
         }
+        // Direct-to-LDS staging addresses each operand through a buffer
+        // resource of 2^31 - 1 bytes (a load past it reads zeros).
+        if ((d.kind == HB_KIND_GEMM || d.kind == HB_KIND_GEMM_SWIGLU) && d.lds_dma) {
+            const uint64_t wb = (d.rows_of == HB_ROWS_DENSE ? 1ull : d.experts) * nw * k * 2;
+            const uint64_t xb = (d.rows_of == HB_ROWS_DENSE || d.rows_of == HB_ROWS_GATHER ? mm : mm * d.top_k) * k * 2;
+            if (wb > 0x7fffffffull || xb > 0x7fffffffull)
+                return fail(HB_ERR_UNSUPPORTED, "gemm (direct-to-LDS staging): W and X at most 2 GiB - 1 bytes each");
+        }
         return HB_OK;
     }
     if (m == 0) return fail(HB_ERR_INVALID, "0 rows");

@@ -185,6 +185,41 @@ def test_gemm_bindings_checked(gpu):
         gpu.free(b)
 
 
+def test_gemm_operands_past_2gib(gpu):
+    """W of 2 GiB (K = N = 32768): the direct-to-LDS forms, whose buffer
+    resources span 2^31 - 1 bytes, refuse it before anything runs; the
+    register-staged form reads every row (rows near the end of W included)
+    and matches the oracle on them (the other rows are zero)."""
+    k = n = 32768
+    m = 16
+    rows = [5, n // 2, n - 3, n - 1]
+    wr = hb.normal_bf16(0x5EED0031, 0.02, (len(rows), k))
+    x = hb.normal_bf16(0x5EED0032, 1.0, (m, k))
+    st = gpu.alloc_with(np.array([0, 0, 0, m], np.uint32))
+    W = gpu.alloc(n * k * 2)
+    X = gpu.alloc_with(x)
+    Y = gpu.alloc(m * n * 2)
+    try:
+        gpu.zero(W)
+        for i, r in enumerate(rows):
+            gpu.upload(W, wr[i], offset=r * k * 2)
+        bind = [hb.r(st), hb.r(W), hb.r(X), hb.r(Y), hb.r(st), hb.r(st)]
+        dma = gpu.pipeline(hb.gemm_mma(k, n, 0, **TILES["t128x128_x16_d2"]))
+        with pytest.raises(hb.HerbertError) as e:
+            gpu.launch(dma, bind, m)
+        assert "2 GiB" in str(e.value)
+        reg = gpu.pipeline(hb.gemm_mma(k, n, 0, **TILES["t64x64_reg_s1"]))
+        gpu.launch(reg, bind, m)
+        gpu.sync()
+        y = gpu.download(Y, np.uint16, m * n).reshape(m, n)
+        check_close(y[:, rows], orc.gemm(x, wr), k, abs_products(x, wr), "2 GiB W rows")
+        others = np.delete(np.arange(n), rows)[::97]
+        assert not np.any(y[:, others] & 0x7fff), "zero rows of W gave nonzero outputs"
+    finally:
+        for b in (st, W, X, Y):
+            gpu.free(b)
+
+
 def test_time_each_brackets_every_launch(gpu):
     """hb_time_each: the per-op means telescope to the whole run's time, and
     the larger GEMM takes longer than the smaller one."""
