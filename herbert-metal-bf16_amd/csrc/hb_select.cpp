@@ -640,7 +640,15 @@ int hb_engine_gemm(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, hb_range 
     std::string what = std::string("gemm ") + key;
     std::vector<Cand> c;
     std::vector<bool> eligible;
+    // Operands past 2 GiB: the direct-to-LDS forms cannot address them (their
+    // buffer resources span 2^31 - 1 bytes); the others run, the first of
+    // them the reference of the check.
+    const bool big = (uint64_t)n * k * 2 > 0x7fffffffull || (uint64_t)m * k * 2 > 0x7fffffffull;
     auto add = [&](const std::string& name, const hb_desc& d) {
+        if (big && d.kind == HB_KIND_GEMM && d.lds_dma) {
+            e->logf("[autotune] gemm %s: %s skipped (operands past 2 GiB)", key, name.c_str());
+            return;
+        }
         int32_t kk;
         int r = e->build(d, &kk);
         if (r) {
@@ -651,7 +659,7 @@ int hb_engine_gemm(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, hb_range 
         eligible.push_back(true);
     };
     for (const auto& f : kForms) add(f.name, form_desc(f, k, n, out, mf));
-    if (c.empty() || c[0].name != "mma")
+    if (c.empty() || (!big && c[0].name != "mma"))
         return fail(HB_ERR_COMPILE, what + ": the production kernel mma is not built: " + hb_last_error());
     for (const auto& f : kMoreForms) add(f.name, form_desc(f, k, n, out, mf));
     for (auto tm_tn : {std::make_pair(64u, 64u), std::make_pair(64u, 32u), std::make_pair(32u, 64u),
@@ -701,7 +709,10 @@ int hb_engine_gate_up(hb_engine* e, uint32_t h, uint32_t inter, hb_range state, 
         *swiglu_kernel = b;
         return HB_OK;
     };
-    if (fswi == 0 || (fswi == 2 && !timed) || h % 32) return keep(gk, sk);
+    // The fused forms stage through LDS directly: W and X within 2 GiB.
+    if (fswi == 0 || (fswi == 2 && !timed) || h % 32 || 4ull * inter * h > 0x7fffffffull ||
+        2ull * m * h > 0x7fffffffull)
+        return keep(gk, sk);
     bool mf = t["gemm.mfirst"] != 0;
     std::string what = std::string("gate_up+swiglu ") + key;
     std::vector<Cand> c;

@@ -215,6 +215,20 @@ def test_gemm_operands_past_2gib(gpu):
         check_close(y[:, rows], orc.gemm(x, wr), k, abs_products(x, wr), "2 GiB W rows")
         others = np.delete(np.arange(n), rows)[::97]
         assert not np.any(y[:, others] & 0x7fff), "zero rows of W gave nonzero outputs"
+        # The selection skips the direct-to-LDS forms for this shape and
+        # picks, checks and times the others.
+        e = hb.Engine(gpu, "")
+        try:
+            kern = e.gemm(k, n, 0, hb.r(st), hb.r(W), hb.r(X), hb.r(Y), m)
+            assert "_dma" not in gpu.kernel_name(kern)
+            assert "skipped (operands past 2 GiB)" in e.log()
+            gpu.zero(Y)
+            gpu.launch(kern, bind, m)
+            gpu.sync()
+            y2 = gpu.download(Y, np.uint16, m * n).reshape(m, n)
+            check_close(y2[:, rows], orc.gemm(x, wr), k, abs_products(x, wr), "2 GiB W rows, picked")
+        finally:
+            e.close()
     finally:
         for b in (st, W, X, Y):
             gpu.free(b)
