@@ -137,7 +137,7 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
     // (correctly rounded); x' = bf16((x * inv) * w) with w + 1 for plus_one.
     static_assert(K % 256 == 0, "XSrc::Norm: K a multiple of 256");
     __shared__ float nred[WAVES * MV];
-    {
+    auto prologue = [&]() HB_INLINE2 {
         constexpr u32 PER = K / 256;
 #pragma unroll
         for (u32 j = 0; j < MV; j++) {
@@ -169,7 +169,7 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
             }
         }
         __syncthreads();
-    }
+    };
 #endif
     // 8 bf16 of x row jj at element `off` from memory (XSrc: plain, swiglu'd).
     auto xmem = [&](u32 jj, u32 off) HB_INLINE2 -> u32x4 {
@@ -188,11 +188,24 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
 #if HB_XLDS && HB_XSRC != 2
     // Every x row's 16-byte chunks into LDS once (rows past m repeat row
     // m-1, as the loads below would).
-    for (u32 c = tid; c < MV * K / 8; c += NT) {
-        const u32 j = c / (K / 8), jj = j < m ? j : m - 1;
-        xn4[c] = xmem(jj, (c % (K / 8)) * 8);
-    }
-    __syncthreads();
+    auto prologue = [&]() HB_INLINE2 {
+        for (u32 c = tid; c < MV * K / 8; c += NT) {
+            const u32 j = c / (K / 8), jj = j < m ? j : m - 1;
+            xn4[c] = xmem(jj, (c % (K / 8)) * 8);
+        }
+        __syncthreads();
+    };
+#endif
+    // x in LDS: the prologue fills it once per workgroup.  XSrc::Norm's
+    // (two passes over x, a reduction) without persistent workgroups runs
+    // after the first W block's loads are issued, whose HBM latency then
+    // covers it; otherwise first (measured: hoisting the short staging of
+    // plain x, or a prologue a persistent workgroup amortises, lost 1-15%).
+    // The MFMA form reads x from memory.
+    constexpr bool HOIST = HB_XSRC == 2 && HB_PERSIST == 0;
+    bool pending = HB_XIN_LDS && HB_FORM != 1 && HOIST;
+#if HB_XIN_LDS
+    if constexpr (!HOIST) prologue();
 #endif
     auto xload = [&](u32 jj, u32 off) HB_INLINE2 -> u32x4 {
 #if HB_XIN_LDS
@@ -242,6 +255,12 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
                     wv[u][r] = on ? __builtin_nontemporal_load((const u32x4*)(wr[r] + k0 + (c0 + 64 * u) * 8))
                                   : u32x4{0u, 0u, 0u, 0u};
             }
+#if HB_XIN_LDS
+            if (HOIST && pending) {
+                prologue();
+                pending = false;
+            }
+#endif
 #pragma unroll
             for (u32 u = 0; u < U; u++) {
                 if (!decltype(full)::value && u * 64 >= REM) break;  // no lane has this chunk
