@@ -229,7 +229,7 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
             e->threads = 1024;
             e->nbind = 4;
             e->defines = {D("HB_OP", atomic ? 3 : 2), D("HB_E", d.experts), D("HB_TOPK", d.top_k),
-                          D("HB_BM", d.bm), D("HB_D", 8)};
+                          D("HB_BM", d.bm), D("HB_D", 8), D("HB_RMAX", d.rows_max)};
             return HB_OK;
         }
         case HB_KIND_GATHER:

@@ -13,7 +13,8 @@
 //             gate, the experts' and shared sums, the residual add)
 //   8 rmsnorm (src/metal/kernels.rs:48-103: the block's input norm)
 // Constants: HB_OP, HB_E (experts), HB_TOPK, HB_BM (rows per expert tile),
-// HB_TILES (table capacity), HB_D (row width: hidden, or n of SwiGLU).
+// HB_TILES (table capacity), HB_D (row width: hidden, or n of SwiGLU),
+// HB_RMAX (sort: rows of the largest block).
 #include "hb_common.h"
 
 #ifndef HB_EPS
@@ -113,8 +114,16 @@ extern "C" __global__ __launch_bounds__(256) void HB_NAME(const u16* __restrict_
 // list[p] = pair row*TOPK + slot grouped by expert, experts ascending;
 // tiles[0] = tile count, tile t = tiles[1+3t..] = (expert, first sorted
 // row, rows <= BM).  Rows = state[3], at most the launch's m.
+// A thread's pairs: scan form, wave w's contiguous range [lo, hi) with lane
+// l taking lo + l + 64k (the pairs of an expert then land in pair order);
+// atomic form, tid + 1024k.  Up to 32 per thread (HB_RMAX * TOPK <= 32768
+// pairs) their experts are read once, all loads issued together, and kept
+// in registers for both passes; beyond that they are read in each pass.
 static_assert(E <= 1024, "sort: at most 1024 experts");
 constexpr u32 BM = HB_BM, NW = 16;
+constexpr u32 PMAX = HB_RMAX * TOPK, PER = (PMAX + 1023) / 1024;
+constexpr bool HOLD = PER <= 32;
+constexpr u32 EPL = (E + 63) / 64;  // experts per lane of the scans
 
 extern "C" __global__ __launch_bounds__(1024) void HB_NAME(const u32* __restrict__ state,
                                                              const u32* __restrict__ route,
@@ -129,16 +138,31 @@ extern "C" __global__ __launch_bounds__(1024) void HB_NAME(const u32* __restrict
         u32 x = route[(i / TOPK) * 2 * TOPK + i % TOPK];
         return x < E ? x : E - 1;
     };
+#if HB_OP == 2
+    const u32 cp = (pairs + NW - 1) / NW;
+    const u32 lo = w * cp < pairs ? w * cp : pairs, hi = lo + cp < pairs ? lo + cp : pairs;
+    auto pair_k = [&](u32 k) -> u32 { return lo + lane + 64 * k; };
+    auto in_k = [&](u32 k) -> bool { return pair_k(k) < hi; };
+    u32* const myhist = hist[w];
+#else
+    auto pair_k = [&](u32 k) -> u32 { return tid + 1024 * k; };
+    auto in_k = [&](u32 k) -> bool { return pair_k(k) < pairs; };
+    u32* const myhist = hist[0];
+#endif
+    u32 ex[HOLD ? PER : 1];
+    if constexpr (HOLD) {
+#pragma unroll
+        for (u32 k = 0; k < PER; k++) ex[k] = in_k(k) ? expert_of(pair_k(k)) : E;
+    }
     for (u32 i = tid; i < NW * E; i += 1024) (&hist[0][0])[i] = 0;
     __syncthreads();
-#if HB_OP == 2
-    // Wave w owns pairs [w*cp, (w+1)*cp): its histogram.
-    const u32 cp = (pairs + NW - 1) / NW;
-    const u32 lo = w * cp, hi = lo + cp < pairs ? lo + cp : pairs;
-    for (u32 i = lo + lane; i < hi; i += 64) atomicAdd(&hist[w][expert_of(i)], 1u);
-#else
-    for (u32 i = tid; i < pairs; i += 1024) atomicAdd(&hist[0][expert_of(i)], 1u);
-#endif
+    if constexpr (HOLD) {
+#pragma unroll
+        for (u32 k = 0; k < PER; k++)
+            if (ex[k] < E) atomicAdd(&myhist[ex[k]], 1u);
+    } else {
+        for (u32 k = 0; in_k(k); k++) atomicAdd(&myhist[expert_of(pair_k(k))], 1u);
+    }
     __syncthreads();
     // Per expert: its count, and each wave's offset inside the expert.
     for (u32 x = tid; x < E; x += 1024) {
@@ -151,17 +175,42 @@ extern "C" __global__ __launch_bounds__(1024) void HB_NAME(const u32* __restrict
         cnt[x] = s;
     }
     __syncthreads();
-    // Expert starts and tile starts (exclusive scans, in expert order).
-    if (tid == 0) {
-        u32 tot = 0, nt = 0;
-        for (u32 x = 0; x < E; x++) {
-            start[x] = tot;
-            tstart[x] = nt;
-            tot += cnt[x];
-            nt += (cnt[x] + BM - 1) / BM;
+    // Expert starts and tile starts: exclusive scans in expert order, by
+    // wave 0 (lane l sums experts l*EPL .., then a prefix over the lanes).
+    if (w == 0) {
+        u32 a = 0, t = 0;
+#pragma unroll
+        for (u32 j = 0; j < EPL; j++) {
+            const u32 x = lane * EPL + j;
+            if (x < E) {
+                a += cnt[x];
+                t += (cnt[x] + BM - 1) / BM;
+            }
         }
-        tstart[E] = nt;
-        tiles[0] = nt;
+        u32 ia = a, it = t;
+#pragma unroll
+        for (u32 sh = 1; sh < 64; sh <<= 1) {
+            const u32 va = __shfl_up(ia, sh, 64), vt = __shfl_up(it, sh, 64);
+            if (lane >= sh) {
+                ia += va;
+                it += vt;
+            }
+        }
+        u32 ea = ia - a, et = it - t;
+#pragma unroll
+        for (u32 j = 0; j < EPL; j++) {
+            const u32 x = lane * EPL + j;
+            if (x < E) {
+                start[x] = ea;
+                tstart[x] = et;
+                ea += cnt[x];
+                et += (cnt[x] + BM - 1) / BM;
+            }
+        }
+        if (lane == 63) {
+            tstart[E] = it;
+            tiles[0] = it;
+        }
     }
     __syncthreads();
     for (u32 x = tid; x < E; x += 1024) {
@@ -179,10 +228,10 @@ extern "C" __global__ __launch_bounds__(1024) void HB_NAME(const u32* __restrict
 #if HB_OP == 2
     // Place the wave's pairs chunk by chunk: a lane's rank among the earlier
     // lanes of the same expert (ballots over the expert's bits).
-    for (u32 base = lo; base < hi; base += 64) {
-        const u32 i = base + lane;
+    auto place = [&](u32 k, u32 x) {
+        const u32 i = pair_k(k);
         const bool on = i < hi;
-        const u32 x = on ? expert_of(i) : E;  // E: matches no real expert
+        if (!on) x = E;  // matches no real expert
         u64 same = __ballot(on);
 #pragma unroll
         for (u32 b = 0; b < 11; b++) {
@@ -201,11 +250,24 @@ extern "C" __global__ __launch_bounds__(1024) void HB_NAME(const u32* __restrict
         if (on && lower == 0) hist[w][x] += (u32)__popcll(same);
         __builtin_amdgcn_s_waitcnt(0);
         __builtin_amdgcn_wave_barrier();
+    };
+    if constexpr (HOLD) {
+#pragma unroll
+        for (u32 k = 0; k < PER; k++)
+            if (lo + 64 * k < hi) place(k, ex[k]);
+    } else {
+        for (u32 k = 0; lo + 64 * k < hi; k++) place(k, pair_k(k) < hi ? expert_of(pair_k(k)) : E);
     }
 #else
-    for (u32 i = tid; i < pairs; i += 1024) {
-        const u32 x = expert_of(i);
-        list[atomicAdd(&hist[0][x], 1u)] = i;
+    if constexpr (HOLD) {
+#pragma unroll
+        for (u32 k = 0; k < PER; k++)
+            if (ex[k] < E) list[atomicAdd(&hist[0][ex[k]], 1u)] = pair_k(k);
+    } else {
+        for (u32 k = 0; in_k(k); k++) {
+            const u32 i = pair_k(k);
+            list[atomicAdd(&hist[0][expert_of(i)], 1u)] = i;
+        }
     }
 #endif
 }

@@ -86,6 +86,30 @@ def test_sort_partial_block(gpu):
     assert np.array_equal(tiles[:used], wt[:used])
 
 
+@pytest.mark.parametrize("experts,top_k,rows,rows_max,bm", [(200, 6, 5000, 8192, 16),
+                                                         (1000, 2, 333, 512, 64),
+                                                         (64, 1, 1, 64, 32)])
+def test_sort_other_shapes(gpu, experts, top_k, rows, rows_max, bm):
+    """Expert counts that are not a multiple of 64 and up to 1024, blocks
+    whose pairs exceed what a thread keeps in registers (8192 rows x 6 slots)
+    and a single row: the scan sort bit for bit, the atomic sort by its
+    invariants."""
+    rng = np.random.default_rng(experts * 7 + top_k)
+    route = np.zeros((rows, 2 * top_k), np.uint32)
+    for r in range(rows):
+        route[r, :top_k] = np.sort(rng.choice(experts, top_k, replace=False))
+        route[r, top_k:] = np.float32(1.0 / top_k).view(np.uint32)
+    lst, tiles = sort_gpu(gpu, route, top_k, experts, bm, rows_max)
+    wl, wt = orc.moe_sort(route, top_k, experts, bm)
+    used = 1 + 3 * int(wt[0])
+    assert np.array_equal(lst, wl)
+    assert np.array_equal(tiles[:used], wt[:used])
+    al, at = sort_gpu(gpu, route, top_k, experts, bm, rows_max, atomic=True)
+    assert np.array_equal(at[:used], wt[:used])
+    assert np.array_equal(route[al // top_k, al % top_k], route[wl // top_k, wl % top_k])
+    assert np.array_equal(np.sort(al), np.arange(rows * top_k))
+
+
 def test_gather_swiglu_combine_bit_exact(gpu):
     rows = 300
     x = hb.normal_bf16(5, 1.0, (rows, H))
