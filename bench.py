@@ -308,9 +308,10 @@ def bench_moe(g, e, hb):
     used = len(np.unique(route[:, :TOPK]))
     P = T * TOPK
     names = ["route", "sort"] + (["gather"] if layer.kernels[3] >= 0 else []) + \
-        ["gate_up", "swiglu", "down", "combine"]
+        ["gate_up"] + ([] if layer.fused else ["swiglu"]) + ["down", "combine"]
     per = dict(zip(names, each))
-    gu_b = 2.0 * used * 2 * MI * H + 2.0 * P * H + 2.0 * P * 2 * MI
+    # gate_up writes EGU (2*MI per pair), or EHB (MI per pair) with the SwiGLU fused.
+    gu_b = 2.0 * used * 2 * MI * H + 2.0 * P * H + 2.0 * P * (MI if layer.fused else 2 * MI)
     dn_b = 2.0 * used * H * MI + 2.0 * P * MI + 2.0 * P * H
     gu_f, dn_f = 2.0 * P * 2 * MI * H, 2.0 * P * H * MI
     out = {"unit": "GB/s", "peak": HBM_PEAK, "layer_us": round(t / reps * 1e6, 2),
@@ -318,7 +319,7 @@ def bench_moe(g, e, hb):
            "gate_up": {"us": round(per["gate_up"] * 1e6, 2), "gbs": round(gu_b / per["gate_up"] / 1e9, 1),
                        "frac": round(gu_b / per["gate_up"] / 1e9 / HBM_PEAK, 4),
                        "tflops": round(gu_f / per["gate_up"] / 1e12, 1),
-                       "kernel": g.kernel_name(layer.kernels[1])},
+                       "kernel": g.kernel_name(layer.kernels[1]), "swiglu_fused": layer.fused},
            "down": {"us": round(per["down"] * 1e6, 2), "gbs": round(dn_b / per["down"] / 1e9, 1),
                     "frac": round(dn_b / per["down"] / 1e9 / HBM_PEAK, 4),
                     "tflops": round(dn_f / per["down"] / 1e12, 1),

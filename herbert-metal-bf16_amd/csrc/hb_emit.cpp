@@ -78,8 +78,8 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
             const bool swi = d.kind == HB_KIND_GEMM_SWIGLU;
             if (d.rows_of > HB_ROWS_SORTED || d.out > HB_OUT_RESIDUAL)
                 return fail(HB_ERR_INVALID, "gemm: rows_of/out out of range");
-            if (swi && (d.rows_of != HB_ROWS_DENSE || d.out != HB_OUT_BF16))
-                return fail(HB_ERR_UNSUPPORTED, "gemm_swiglu: dense rows, bf16 out");
+            if (swi && (d.rows_of == HB_ROWS_SCATTER || d.out != HB_OUT_BF16))
+                return fail(HB_ERR_UNSUPPORTED, "gemm_swiglu: dense or gathered rows, bf16 out");
             if (d.band && d.rows_of != HB_ROWS_DENSE)
                 return fail(HB_ERR_UNSUPPORTED, "gemm: band order over dense rows only");
             if (d.mfma != 16 && d.mfma != 32) return fail(HB_ERR_UNSUPPORTED, "gemm: mfma 16 or 32");

@@ -397,6 +397,11 @@ uint32_t hb_kernel_bindings(hb_gpu* g, int32_t kernel) {
     return g->kernels[kernel].em.nbind;
 }
 
+uint32_t hb_kernel_kind(hb_gpu* g, int32_t kernel) {
+    if (kernel < 0 || (size_t)kernel >= g->kernels.size()) return 0;
+    return g->kernels[kernel].desc.kind;
+}
+
 double hb_compile_seconds(hb_gpu* g) { return g->compile_seconds; }
 
 int hb_launch(hb_gpu* g, int32_t kernel, const hb_range* b, uint32_t nbind, uint32_t m) {

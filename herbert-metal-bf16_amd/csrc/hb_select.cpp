@@ -933,6 +933,13 @@ int hb_engine_experts(hb_engine* e, uint32_t experts, uint32_t top_k, uint32_t h
         *bm_out = bm;
         return HB_OK;
     }
+    // swiglu_slots after an unfused gate|up (EGU -> EHB), timed with it.
+    hb_desc swd{};
+    swd.kind = HB_KIND_SWIGLU;
+    swd.n = inter;
+    int32_t swiglu;
+    if ((rc = e->build(swd, &swiglu))) return rc;
+    const hb_op sw_op = make_op(swiglu, m * top_k, {io->egu, io->ehb});
     auto gu_ops = [&](int32_t k, hb_range xin) {
         return make_op(k, m, {io->state, io->w_gate_up, xin, io->egu, io->list, io->tiles});
     };
@@ -969,8 +976,22 @@ int hb_engine_experts(hb_engine* e, uint32_t experts, uint32_t top_k, uint32_t h
             }
             std::vector<hb_op> ops;
             if (gathered) ops.push_back(g_op);
-            ops.push_back(gu_ops(k, gathered ? io->xs : io->x));
+            if (d.kind == HB_KIND_GEMM_SWIGLU) {
+                // The SwiGLU in the epilogue: EHB written directly.
+                ops.push_back(make_op(k, m, {io->state, io->w_gate_up, gathered ? io->xs : io->x, io->ehb,
+                                             io->list, io->tiles}));
+            } else {
+                ops.push_back(gu_ops(k, gathered ? io->xs : io->x));
+                ops.push_back(sw_op);
+            }
             cgu.push_back({name, k, ops});
+        };
+        // gemm_desc of the fused [gate | up] + SwiGLU form: inter features,
+        // bn W rows (bn/2 features) per tile.
+        auto swi_desc = [&](uint32_t bn, uint32_t wm = 1, uint32_t wn = 4) {
+            hb_desc d = gemm_desc(hidden, inter, HB_ROWS_GATHER, bm, bn, wm, wn);
+            d.kind = HB_KIND_GEMM_SWIGLU;
+            return d;
         };
         auto add_dn = [&](const std::string& name, const hb_desc& d) {
             int32_t k;
@@ -986,6 +1007,9 @@ int hb_engine_experts(hb_engine* e, uint32_t experts, uint32_t top_k, uint32_t h
         add_gu("mma_n256", gemm_desc(hidden, 2 * inter, HB_ROWS_GATHER, bm, 256), false);
         add_gu("gather+mma", gemm_desc(hidden, 2 * inter, HB_ROWS_SORTED, bm, 128), true);
         if (bm >= 32) add_gu("mma_w2x2", gemm_desc(hidden, 2 * inter, HB_ROWS_GATHER, bm, 128, 2, 2), false);
+        add_gu("mma_swiglu", swi_desc(128), false);
+        add_gu("mma_swiglu_n256", swi_desc(256), false);
+        if (bm >= 32) add_gu("mma_swiglu_w2x2", swi_desc(128, 2, 2), false);
         add_dn("mma", gemm_desc(inter, hidden, HB_ROWS_SCATTER, bm, 128));
         add_dn("mma_n256", gemm_desc(inter, hidden, HB_ROWS_SCATTER, bm, 256));
         if (bm >= 32) add_dn("mma_w2x4_s3", gemm_desc(inter, hidden, HB_ROWS_SCATTER, bm, 128, 2, 4, 2));
@@ -1003,7 +1027,7 @@ int hb_engine_experts(hb_engine* e, uint32_t experts, uint32_t top_k, uint32_t h
             kernels[0] = cs[bs].kernel;
             kernels[1] = cgu[bgu].kernel;
             kernels[2] = cdn[bdn].kernel;
-            kernels[3] = cgu[bgu].ops.size() > 1 ? gather : -1;
+            kernels[3] = cgu[bgu].ops[0].kernel == gather ? gather : -1;
             *bm_out = bm;
         }
     }

@@ -37,9 +37,11 @@
 // HB_BK, HB_WM, HB_WN, HB_MFMA (16|32), HB_STAGES (1..4), HB_SWZ, HB_ORDER,
 // HB_MFIRST, HB_DMA, HB_SWIGLU, HB_BAND (the tile order band).
 //
-// HB_SWIGLU 1 (dense rows, Bf16): the [gate | up] projection and the SwiGLU
-// in one (prefill.rs:755-824, gemm_nax_swiglu).  N is the feature count nf
-// and W holds 2*nf rows (gate rows, then their up rows); a tile covers BN/2
+// HB_SWIGLU 1 (dense or gathered rows, Bf16): the [gate | up] projection and
+// the SwiGLU in one (prefill.rs:755-824, gemm_nax_swiglu; for the experts,
+// the grouped gate|up and swiglu_slots, qwen_kernels.rs:2087-2117).  N is the
+// feature count nf and W holds 2*nf rows per expert (gate rows, then their
+// up rows); a tile covers BN/2
 // features: each wave's W fragments 0..IN/2-1 are gate rows and fragments
 // IN/2.. the up rows of the same features, so a lane holds the gate and the
 // up sums of the same outputs and writes h = rne(g * sigmoid(g) * u) with g,
@@ -89,8 +91,8 @@ static_assert(BK % KS == 0 && (CH & (CH - 1)) == 0, "K step");
 static_assert(NT % CH == 0, "threads a multiple of the chunks of a row");
 static_assert(NS >= 1 && NS <= 4, "1 to 4 stages");
 static_assert(HB_DMA || NS <= 2, "register staging: 1 or 2 stages");
-static_assert(!SWI || (IN % 2 == 0 && OUT == 0 && ROWS == 0),
-              "fused SwiGLU: dense rows, bf16 out, an even count of W fragments per wave");
+static_assert(!SWI || (IN % 2 == 0 && OUT == 0 && ROWS != 2),
+              "fused SwiGLU: dense or gathered rows, bf16 out, an even count of W fragments per wave");
 
 typedef __attribute__((ext_vector_type(FM == 16 ? 4 : 16))) float acc_t;
 
@@ -239,7 +241,7 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
             const u32 t = r % TN, i = t / FM, up = i >= IN / 2 ? 1u : 0u;
             u32 f = n0 + (r / TN) * (TN / 2) + (i - up * (IN / 2)) * FM + t % FM;
             f = f < N ? f : N - 1;
-            return up * N + f;
+            return (expert * 2 + up) * N + f;  // an expert's [gate | up] rows
         }
         u32 n = n0 + r;
         return expert * N + (n < N ? n : N - 1);

@@ -170,6 +170,8 @@ lib.hb_kernel_groups.argtypes = [_P, _i32, _u32]
 lib.hb_kernel_groups.restype = _u32
 lib.hb_kernel_bindings.argtypes = [_P, _i32]
 lib.hb_kernel_bindings.restype = _u32
+lib.hb_kernel_kind.argtypes = [_P, _i32]
+lib.hb_kernel_kind.restype = _u32
 lib.hb_compile_seconds.argtypes = [_P]
 lib.hb_compile_seconds.restype = ctypes.c_double
 lib.hb_launch.argtypes = [_P, _i32, ctypes.POINTER(Range), _u32, _u32]
@@ -359,6 +361,9 @@ class Gpu:
     def kernel_name(self, k):
         return lib.hb_kernel_name(self.h, int(k)).decode()
 
+    def kernel_kind(self, k):
+        return lib.hb_kernel_kind(self.h, int(k))
+
     def groups(self, k, m):
         return lib.hb_kernel_groups(self.h, int(k), int(m))
 
@@ -496,7 +501,8 @@ class Engine:
 class MoeLayer:
     """The routed experts of one MoE layer over blocks of up to `rows` rows,
     in the reference's op order (qwen.rs:2705-2735): route_qwen -> moe_sort
-    -> [moe_gather] -> grouped gate|up -> swiglu_slots -> grouped down
+    -> [moe_gather] -> grouped gate|up -> swiglu_slots (or fused into the
+    gate|up, when the selection picked that form) -> grouped down
     (scatter to slot rows) -> moe_combine.  Owns its device buffers; the
     kernels come from Engine.experts (expert_pipes), timed on the route of
     `scores` ([rows][experts] bf16, routed here first: the reference's
@@ -535,6 +541,7 @@ class MoeLayer:
             g.launch(self.route_k, [r(b["scores"]), r(b["route"])], rows)
             g.sync()
         self.kernels, self.bm = engine.experts(experts, top_k, hidden, inter, rows, self.io)
+        self.fused = gpu.kernel_kind(self.kernels[1]) == Kind.GEMM_SWIGLU
 
     def ops(self, m=None):
         """The layer's dispatches over m rows (m <= rows; state[3] must be m)."""
@@ -547,9 +554,14 @@ class MoeLayer:
         if gather >= 0:
             ops.append(Op(gather, [r(b["state"]), r(b["list"]), r(b["x"]), r(b["xs"])], m))
             xin = b["xs"]
-        ops.append(Op(gu, [r(b["state"]), r(b["w_gate_up"]), r(xin), r(b["egu"]), r(b["list"]),
-                           r(b["tiles"])], m))
-        ops.append(Op(self.swiglu_k, [r(b["egu"]), r(b["ehb"])], m * k))
+        if self.fused:
+            # The grouped gate|up writes the SwiGLU itself.
+            ops.append(Op(gu, [r(b["state"]), r(b["w_gate_up"]), r(xin), r(b["ehb"]), r(b["list"]),
+                               r(b["tiles"])], m))
+        else:
+            ops.append(Op(gu, [r(b["state"]), r(b["w_gate_up"]), r(xin), r(b["egu"]), r(b["list"]),
+                               r(b["tiles"])], m))
+            ops.append(Op(self.swiglu_k, [r(b["egu"]), r(b["ehb"])], m * k))
         ops.append(Op(dn, [r(b["state"]), r(b["w_down"]), r(b["ehb"]), r(b["ey"]), r(b["list"]),
                            r(b["tiles"])], m))
         ops.append(Op(self.combine_k, [r(b["ey"]), r(b["route"]), r(b["out"])], m))

@@ -167,6 +167,10 @@ const char *hb_kernel_name(hb_gpu *gpu, int32_t kernel);
 uint32_t hb_kernel_groups(hb_gpu *gpu, int32_t kernel, uint32_t m);
 /* Bindings the kernel takes, in order (Emitted::bindings). */
 uint32_t hb_kernel_bindings(hb_gpu *gpu, int32_t kernel);
+/* The kernel's descriptor kind (enum hb_kind; 0 for no such kernel): the
+ * Rust side keeps its pipelines' kinds itself; here it tells a caller of
+ * hb_engine_experts whether the gate|up kernel writes the SwiGLU. */
+uint32_t hb_kernel_kind(hb_gpu *gpu, int32_t kernel);
 /* Seconds spent compiling so far ([metal] line, qwen.rs:1069). */
 double hb_compile_seconds(hb_gpu *gpu);
 
@@ -273,7 +277,10 @@ int hb_engine_matvec_fused(hb_engine *engine, uint32_t k, uint32_t n, uint32_t o
  * EHB [m*top_k][inter], down W [experts*hidden][inter], EY
  * [m*top_k][hidden], XS [m*top_k][hidden] (the gather's output).
  * kernels[0..3] = sort, gate_up GEMM, down GEMM, gather (-1: gate_up reads
- * X through the list itself); *bm = rows per tile. */
+ * X through the list itself); *bm = rows per tile.  A gate_up kernel of kind
+ * HB_KIND_GEMM_SWIGLU has swiglu_slots fused: it writes EHB (bind EHB as
+ * its Y) and no SwiGLU pass runs; else it writes EGU and swiglu_slots
+ * (HB_KIND_SWIGLU, EGU -> EHB over m*top_k rows) follows. */
 typedef struct hb_moe_io {
     hb_range state, route, list, tiles, x, w_gate_up, egu, ehb, w_down, ey, xs;
 } hb_moe_io;

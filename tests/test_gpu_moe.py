@@ -183,3 +183,38 @@ def test_grouped_gemm_gather_and_scatter(gpu, tname, bm):
         sel = np.nonzero(ex == e)[0]
         ap[lst[sel]] = abs_products(xs[sel], wd[e * H:(e + 1) * H])
     check_close(got, want, MI, ap, "down " + tname)
+
+
+@pytest.mark.parametrize("bm,bn,wm,wn", [(32, 128, 1, 4), (128, 128, 2, 2), (64, 256, 1, 4)])
+def test_grouped_gate_up_swiglu_fused(gpu, bm, bn, wm, wn):
+    """The grouped gate|up with swiglu_slots in its epilogue: bit-equal to the
+    same tile form's GEMM (EGU) followed by swiglu_slots (the sums run the
+    same MFMA sequence), over the bench's route; rows of each expert's
+    [gate | up] W."""
+    rows, experts, top_k, hidden, inter = 512, 64, 4, 512, 256
+    scores = hb.normal_bf16(0x5EED0041, 1.0, (rows, experts))
+    route = orc.route(scores, top_k)
+    lst, tiles = sort_gpu(gpu, route, top_k, experts, bm, rows)
+    x = hb.normal_bf16(0x5EED0042, 1.0, (rows, hidden))
+    w = hb.normal_bf16(0x5EED0043, 0.05, (experts * 2 * inter, hidden))
+    P = rows * top_k
+    nt = hb.moe_tiles(rows, top_k, experts, bm)
+    st = np.array([0, 0, 0, rows], np.uint32)
+    tile = dict(bm=bm, bn=bn, bk=64, wm=wm, wn=wn, mfma=16, dbuf=1, lds_dma=1, order=0)
+    common = dict(top_k=top_k, tiles=nt, experts=experts, rows_max=rows)
+    d = hb.gemm_mma_rows(hidden, 2 * inter, 0, True, hb.Rows.Gather, **common, **tile)
+    egu = launch(gpu, d, [st, w, x, P * 2 * inter * 2, lst, tiles], rows,
+                 {3: (np.uint16, P * 2 * inter)})[3].reshape(P, 2 * inter)
+    want = launch(gpu, hb.swiglu_rows(inter), [egu, P * inter * 2], P, {1: (np.uint16, P * inter)})[1]
+    ds = hb.Desc(kind=hb.Kind.GEMM_SWIGLU, k=hidden, n=inter, out=0, m_first=True, rows_of=hb.Rows.Gather,
+                 **common, **tile)
+    got = launch(gpu, ds, [st, w, x, P * inter * 2, lst, tiles], rows, {3: (np.uint16, P * inter)})[3]
+    assert np.array_equal(got, want), "fused grouped gate|up+SwiGLU != GEMM then swiglu_slots"
+    # And the unfused GEMM within the contract of the oracle on sampled pairs.
+    sel = np.arange(0, P, 37)
+    xr = x[lst[sel] // top_k]
+    ex = route[lst[sel] // top_k, lst[sel] % top_k]
+    for i, p in enumerate(sel):
+        wr = w[ex[i] * 2 * inter:(ex[i] + 1) * 2 * inter]
+        check_close(egu[p:p + 1], orc.gemm(xr[i:i + 1], wr), hidden, abs_products(xr[i:i + 1], wr),
+                    "pair %d" % p)
