@@ -27,6 +27,11 @@ profiles/traffic.json, written from two counter runs of this file:
     rocprofv3 --pmc WRITE_SIZE -d W -o run --output-format csv -- python3 bench.py --traffic-run
     python3 bench.py --traffic-summary F/run_counter_collection.csv W/run_counter_collection.csv
 
+The kernel-trace summary in profiles/ comes from
+
+    rocprofv3 --kernel-trace --stats -d P -o bench --output-format csv -- python3 bench.py --steps 20 > B
+    python3 bench.py --trace-summary P/bench_kernel_trace.csv B '<that rocprofv3 command>'
+
 --traffic-run selects the step's kernels (every candidate is dispatched, so
 every candidate gets counters) and copies COPY_BYTES device to device; the
 summary scales each kernel's FETCH_SIZE and WRITE_SIZE (KiB per dispatch)
@@ -96,9 +101,13 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--traffic-run", action="store_true")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
+    ap.add_argument("--trace-summary", nargs=3, metavar=("TRACE_CSV", "BENCH_OUT", "COMMAND"))
     args = ap.parse_args()
     if args.traffic_summary:
         traffic_summary(*args.traffic_summary)
+        return
+    if args.trace_summary:
+        trace_summary(*args.trace_summary)
         return
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only (--gpus %d asked); the path would shard "
@@ -244,6 +253,75 @@ def traffic_run(g, ops, per_gemm):
     g.free(b)
     print(json.dumps({"picked": {nm: d["kernel"] for nm, d in per_gemm.items()},
                       "copy_bytes": COPY_BYTES}), flush=True)
+
+
+def trace_summary(trace_csv, bench_json, cmd):
+    """The profiles/ summary of a `rocprofv3 --kernel-trace --stats` run of
+    this file (its kernel_trace CSV; kernel_stats beside it) and the JSON
+    line that run printed: the step's four GEMMs in the timed regions (the
+    last 2*steps consecutive steps of them in the trace) against the bench's
+    own times, the decode and MoE kernels, the top kernels by total time."""
+    import csv
+    import statistics
+    b = json.loads([ln for ln in open(bench_json) if ln.startswith("{")][-1])
+    rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
+
+    def dur(r):
+        return (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+
+    gem = ("qkv", "o", "gate_up", "down")
+    names = [b["config"]["gemms"][g]["kernel"] for g in gem]
+    seq = [r["Kernel_Name"] for r in rows]
+    best, bi, i = 0, 0, 0
+    while i < len(seq):
+        j = i
+        while j + 3 < len(seq) and seq[j:j + 4] == names:
+            j += 4
+        if (j - i) // 4 > best:
+            best, bi = (j - i) // 4, i
+        i = j + 1 if j == i else j
+    steps = b["steps"]
+    last = rows[bi + 4 * (best - steps):bi + 4 * best]  # the per-launch event region
+    first = rows[bi + 4 * (best - 2 * steps):bi + 4 * (best - steps)]  # the step-time region
+
+    def span(rr):
+        return (int(rr[-1]["End_Timestamp"]) - int(rr[0]["Start_Timestamp"])) / 1e3 / steps
+
+    def avg_of(nm, n=40):
+        d = [dur(r) for r in rows if r["Kernel_Name"] == nm]
+        return len(d), statistics.mean(d[-n:]) if d else float("nan")
+
+    out = ["command: cd /tmp && TMPDIR=/tmp " + cmd,
+           "summary: python3 bench.py --trace-summary <the run's kernel_trace.csv> <its stdout> '<command>'",
+           "bench line (same run): value %.1f TFLOP/s, ms_per_step %.4f, roofline.frac %.4f (%s)" % (
+               b["value"], b["ms_per_step"], b["roofline"]["frac"], b["roofline"]["gemm"]), "",
+           "main step (configs[1], M=2048): %d consecutive steps of the 4 GEMMs found in the trace" % best,
+           "  step-time region (%d steps, events at the ends only): rocprof first-start..last-end %.1f "
+           "us/step, bench %.1f us/step" % (steps, span(first), b["ms_per_step"] * 1e3)]
+    for g, nm in zip(gem, names):
+        d1 = [dur(r) for r in first if r["Kernel_Name"] == nm]
+        d2 = [dur(r) for r in last if r["Kernel_Name"] == nm]
+        out.append("  %-8s %-66s rocprof avg %7.2f us (step region) %7.2f us (event region) | bench event "
+                   "avg %7.2f us" % (g, nm, statistics.mean(d1), statistics.mean(d2), b["config"]["gemms"][g]["us"]))
+    mv = b.get("matvec")
+    if mv:
+        out += ["", "decode (M=1) kernels, rocprof average of their last 40 dispatches:"]
+        for g, nm in mv["kernels"].items():
+            n, a = avg_of(nm)
+            out.append("  %-8s %-52s calls %5d  avg %7.2f us" % (g, nm, n, a))
+    moe = b.get("moe")
+    if moe:
+        out += ["", "MoE layer (config 5): bench per-op times, and the grouped GEMMs' rocprof averages:"]
+        out.append("  " + ", ".join("%s %.2f us" % kv for kv in moe["ops_us"].items()))
+        for g in ("gate_up", "down"):
+            n, a = avg_of(moe[g]["kernel"])
+            out.append("  %-8s %-80s calls %5d  avg %7.2f us" % (g, moe[g]["kernel"], n, a))
+    stats = list(csv.DictReader(open(trace_csv.replace("kernel_trace", "kernel_stats"))))
+    out += ["", "top kernels by total time (the load-time selection's candidates included):"]
+    for r in stats[:15]:
+        out.append("  %-70s calls %6s avg %9.2f us %5.1f%%" % (r["Name"][:70], r["Calls"],
+                                                             float(r["AverageNs"]) / 1e3, float(r["Percentage"])))
+    print("\n".join(out))
 
 
 def traffic_summary(fetch_csv, write_csv):
