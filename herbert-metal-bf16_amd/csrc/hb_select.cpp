@@ -250,10 +250,13 @@ const Form kForms[10] = {
 // fill whole rounds of the 256 CUs on this build's shapes (256 x 192:
 // 768 tiles at 2048 x 18432; 128 x 160: 256 at 2048 x 2560; 128 x 192:
 // 224 at 2048 x 2560, 8 wavefronts), three and four stages of 64 K for the
-// long-K shapes, and the band tile order of gemm_nax (prefill.rs:615-631).
+// long-K shapes, and the band tile order of gemm_nax (prefill.rs:615-631):
+// with bands of 4 row tiles each XCD's 32 concurrent 256 x 192 tiles are 4
+// row tiles by 8 column tiles, fewer compulsory L2 misses than 8 by 4.
 const Form kMoreForms[] = {
     {"mma_t256x192_w8", 256, 192, 64, 4, 2, 32, 1, 1, 1},
     {"mma_t256x192_w8_x16", 256, 192, 64, 4, 2, 16, 1, 1, 1},
+    {"mma_t256x192_w8_x16_b4", 256, 192, 64, 4, 2, 16, 1, 1, 1, 4},
     {"mma_t128x160", 128, 160, 64, 2, 2, 16, 1, 1, 1},
     {"mma_t128x160_s4", 128, 160, 64, 2, 2, 16, 3, 1, 0},
     {"mma_t128x192_w8_s3", 128, 192, 64, 2, 4, 16, 2, 1, 0},
