@@ -262,6 +262,8 @@ const Form kMoreForms[] = {
     {"mma_t128x192_w8_s3", 128, 192, 64, 2, 4, 16, 2, 1, 0},
     {"mma_t128x192_w8_s4", 128, 192, 64, 2, 4, 16, 3, 1, 0},
     {"mma_t128x192_w8_s4_b2", 128, 192, 64, 2, 4, 16, 3, 1, 0, 2},
+    {"mma_t128x192_w8_s4_o1_b4", 128, 192, 64, 2, 4, 16, 3, 1, 1, 4},
+    {"mma_t128x160_s4_o1_b4", 128, 160, 64, 2, 2, 16, 3, 1, 1, 4},
     {"mma_t256x128_w8_s3", 256, 128, 64, 4, 2, 16, 2, 1, 1},
     {"mma_b2", 128, 128, 64, 2, 2, 16, 1, 1, 0, 2},
 };
