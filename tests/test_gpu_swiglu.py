@@ -125,11 +125,15 @@ def test_fused_swiglu_config2_gate_up(gpu):
 
 
 def test_fused_swiglu_refusals(gpu):
-    """Odd W fragments per wave, expert rows and non-bf16 out are refused."""
+    """Odd W fragments per wave, scattered expert rows and non-bf16 out are
+    refused (gathered expert rows are the grouped gate|up's fused form)."""
     with pytest.raises(hb.HerbertError, match="even count"):
         gpu.pipeline(hb.gemm_mma_swiglu(256, 512, bm=128, bn=96, wm=2, wn=2, mfma=16))
-    with pytest.raises(hb.HerbertError, match="dense rows"):
+    with pytest.raises(hb.HerbertError, match="bf16 out"):
         gpu.pipeline(hb.Desc(kind=hb.Kind.GEMM_SWIGLU, k=256, n=512, out=hb.Out.F32))
+    with pytest.raises(hb.HerbertError, match="dense or gathered rows"):
+        gpu.pipeline(hb.Desc(kind=hb.Kind.GEMM_SWIGLU, k=256, n=512, out=hb.Out.Bf16,
+                             rows_of=hb.Rows.Scatter, top_k=8, experts=64, tiles=100, rows_max=64))
 
 
 @pytest.mark.parametrize("fswi", [0, 1, 2])
