@@ -1012,11 +1012,25 @@ int hb_engine_experts(hb_engine* e, uint32_t experts, uint32_t top_k, uint32_t h
         add_gu("mma_n256", gemm_desc(hidden, 2 * inter, HB_ROWS_GATHER, bm, 256), false);
         add_gu("gather+mma", gemm_desc(hidden, 2 * inter, HB_ROWS_SORTED, bm, 128), true);
         if (bm >= 32) add_gu("mma_w2x2", gemm_desc(hidden, 2 * inter, HB_ROWS_GATHER, bm, 128, 2, 2), false);
+        {
+            hb_desc d = gemm_desc(hidden, 2 * inter, HB_ROWS_GATHER, bm, 128);
+            d.m_first = !d.m_first;
+            add_gu(d.m_first ? "mma_mf" : "mma_nf", d, false);
+            hb_desc ds = swi_desc(128);
+            ds.m_first = !ds.m_first;
+            add_gu(ds.m_first ? "mma_swiglu_mf" : "mma_swiglu_nf", ds, false);
+        }
         add_gu("mma_swiglu", swi_desc(128), false);
         add_gu("mma_swiglu_n256", swi_desc(256), false);
         if (bm >= 32) add_gu("mma_swiglu_w2x2", swi_desc(128, 2, 2), false);
         add_dn("mma", gemm_desc(inter, hidden, HB_ROWS_SCATTER, bm, 128));
         add_dn("mma_n256", gemm_desc(inter, hidden, HB_ROWS_SCATTER, bm, 256));
+        {
+            // Column tiles first: the expert tile's 16 column tiles in turn.
+            hb_desc d = gemm_desc(inter, hidden, HB_ROWS_SCATTER, bm, 128);
+            d.m_first = !d.m_first;
+            add_dn(d.m_first ? "mma_mf" : "mma_nf", d);
+        }
         if (bm >= 32) add_dn("mma_w2x4_s3", gemm_desc(inter, hidden, HB_ROWS_SCATTER, bm, 128, 2, 4, 2));
         size_t bgu, bdn;
         double s_gu, s_dn;

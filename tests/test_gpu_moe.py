@@ -131,10 +131,10 @@ def test_gather_swiglu_combine_bit_exact(gpu):
     assert np.array_equal(out.reshape(rows, H), orc.combine(y, route, TOPK, H))
 
 
-def experts_run(gpu, x, w, lst, tiles, k, n, rows_of, rows, bm, **tile):
+def experts_run(gpu, x, w, lst, tiles, k, n, rows_of, rows, bm, m_first=True, **tile):
     pairs = rows * TOPK
     ntiles = hb.moe_tiles(rows, TOPK, E, bm)
-    d = hb.gemm_mma_rows(k, n, 0, True, rows_of, top_k=TOPK, tiles=ntiles, bm=bm, experts=E,
+    d = hb.gemm_mma_rows(k, n, 0, m_first, rows_of, top_k=TOPK, tiles=ntiles, bm=bm, experts=E,
                          rows_max=rows, **tile)
     st = np.array([0, 0, 0, rows], np.uint32)
     tl = np.zeros(1 + 3 * ntiles, np.uint32)
@@ -150,11 +150,13 @@ EXPERT_TILES = {
     "m16_dma": dict(wm=1, wn=4, mfma=16, bn=128, bk=64, dbuf=1, lds_dma=1),
     "m128_w2x2": dict(wm=2, wn=2, mfma=16, bn=128, bk=64, dbuf=1, lds_dma=1),
     "m64_w2x4_s3": dict(wm=2, wn=4, mfma=16, bn=128, bk=64, dbuf=2, lds_dma=1),
+    "m16_dma_nf": dict(wm=1, wn=4, mfma=16, bn=128, bk=64, dbuf=1, lds_dma=1, m_first=False),
 }
 
 
 @pytest.mark.parametrize("tname,bm", [("m16_reg", 16), ("m32_reg_d", 32), ("m64_dma", 64),
-                                      ("m16_dma", 16), ("m128_w2x2", 128), ("m64_w2x4_s3", 64)])
+                                      ("m16_dma", 16), ("m128_w2x2", 128), ("m64_w2x4_s3", 64),
+                                      ("m16_dma_nf", 16)])
 def test_grouped_gemm_gather_and_scatter(gpu, tname, bm):
     """Config 5's grouped gate|up (Gather: sorted row p reads X row
     list[p]/top_k) and down (Scatter: writes row list[p]), on 512 tokens
