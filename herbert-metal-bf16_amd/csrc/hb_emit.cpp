@@ -251,7 +251,8 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
             e->defines = {D("HB_OP", 5), D("HB_E", 64), D("HB_TOPK", 1), D("HB_D", d.n)};
             return HB_OK;
         case HB_KIND_COMBINE:
-            if (!d.n || d.n % 8 || !d.top_k) return fail(HB_ERR_UNSUPPORTED, "combine: d a multiple of 8");
+            if (!d.n || d.n % 8 || !d.top_k || d.top_k > 16)
+                return fail(HB_ERR_UNSUPPORTED, "combine: d a multiple of 8, top_k 1..16");
             snprintf(name, sizeof name, "moe_combine_%u_k%u", d.n, d.top_k);
             e->name = name;
             e->source = "moe.hip";

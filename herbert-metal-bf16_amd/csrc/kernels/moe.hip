@@ -317,7 +317,7 @@ extern "C" __global__ __launch_bounds__(256) void HB_NAME(const u32x4* __restric
 #elif HB_OP == 6
 // ---- combine: out[r] = the slots added in route order, each rounding as
 // index_add_ into a bf16 zero vector: acc = rne(acc + rne(y * w)) ----
-static_assert(D % 8 == 0, "combine: hidden a multiple of 8");
+static_assert(D % 8 == 0 && TOPK <= 16, "combine: hidden a multiple of 8, top_k <= 16");
 constexpr u32 CELLS = D / 8;
 
 extern "C" __global__ __launch_bounds__(256) void HB_NAME(const u32x4* __restrict__ y,
@@ -329,9 +329,19 @@ extern "C" __global__ __launch_bounds__(256) void HB_NAME(const u32x4* __restric
     float acc[8];
 #pragma unroll
     for (u32 e = 0; e < 8; e++) acc[e] = 0.0f;
+    // Every slot's row chunk and weight loaded before the first sum (one
+    // memory latency, not TOPK), then the sums in slot order.
+    u32x4 vs[TOPK];
+    float ws[TOPK];
+#pragma unroll
     for (u32 s = 0; s < TOPK; s++) {
-        const u32x4 v = y[((u64)r * TOPK + s) * CELLS + c];
-        const float w = __builtin_bit_cast(float, route[(u64)r * 2 * TOPK + TOPK + s]);
+        vs[s] = y[((u64)r * TOPK + s) * CELLS + c];
+        ws[s] = __builtin_bit_cast(float, route[(u64)r * 2 * TOPK + TOPK + s]);
+    }
+#pragma unroll
+    for (u32 s = 0; s < TOPK; s++) {
+        const u32x4 v = vs[s];
+        const float w = ws[s];
 #pragma unroll
         for (u32 e = 0; e < 4; e++) {
             acc[2 * e] = round_bf16(acc[2 * e] + round_bf16(bf16_lo(v[e]) * w));
@@ -362,6 +372,7 @@ extern "C" __global__ __launch_bounds__(256) void HB_NAME(const u16* __restrict_
     if (r >= rows) return;
     const u64 base = (u64)r * D;
     float a = 0.0f;
+#pragma unroll
     for (u32 i = t; i < D; i += 256) a = __builtin_fmaf(bf16_to_f32(xn[base + i]), bf16_to_f32(gate[i]), a);
 #pragma unroll
     for (int s = 32; s >= 1; s >>= 1) a += __shfl_xor(a, s, 64);
@@ -369,6 +380,7 @@ extern "C" __global__ __launch_bounds__(256) void HB_NAME(const u16* __restrict_
     __syncthreads();
     const float dot = ((red[0] + red[1]) + red[2]) + red[3];
     const float g = round_bf16(hb_sigmoid(round_bf16(dot)));
+#pragma unroll
     for (u32 i = t; i < D; i += 256) {
         const float s = round_bf16(g * bf16_to_f32(sh[base + i]));
         const float o = round_bf16(bf16_to_f32(ex[base + i]) + s);
@@ -392,6 +404,7 @@ extern "C" __global__ __launch_bounds__(256) void HB_NAME(const u16* __restrict_
     if (r >= rows) return;
     const u64 base = (u64)r * D;
     float a = 0.0f;
+#pragma unroll
     for (u32 i = t; i < D; i += 256) {
         const float v = bf16_to_f32(x[base + i]);
         a = __builtin_fmaf(v, v, a);
@@ -403,6 +416,7 @@ extern "C" __global__ __launch_bounds__(256) void HB_NAME(const u16* __restrict_
     const float ss = ((red[0] + red[1]) + red[2]) + red[3];
     const float inv_d = 1.0f / (float)D, eps = __uint_as_float((u32)HB_EPS);
     const float inv = __fdiv_rn(1.0f, __fsqrt_rn(ss * inv_d + eps));
+#pragma unroll
     for (u32 i = t; i < D; i += 256) {
         float wf = bf16_to_f32(w[i]);
         if (HB_PLUS1) wf = wf + 1.0f;
