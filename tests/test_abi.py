@@ -86,3 +86,19 @@ def test_library_fails_loudly_without_build(tmp_path):
                         "import builtins, os; os.path.exists = lambda p: False if p.endswith('libherbert_hip.so') else True; import herbert_hip")],
                        capture_output=True, text=True, env=env)
     assert r.returncode != 0 and "not built" in r.stderr
+
+
+CLI = os.path.join(ROOT, "herbert-metal-bf16_amd", "hb_gemm")
+
+
+def test_native_cli_usage_and_no_device():
+    """hb_gemm (a C++ host linked against the library): usage on no shapes or
+    a bad one (status 2); without a GPU the library's error, status 1."""
+    r = subprocess.run([CLI], capture_output=True, text=True)
+    assert r.returncode == 2 and "usage" in r.stderr
+    r = subprocess.run([CLI, "12x34"], capture_output=True, text=True)
+    assert r.returncode == 2 and "bad shape" in r.stderr
+    if os.environ.get("HIP_VISIBLE_DEVICES") is None and os.path.exists("/dev/kfd"):
+        pytest.skip("a GPU is visible")
+    r = subprocess.run([CLI, "64x128x256"], capture_output=True, text=True)
+    assert r.returncode == 1 and "no HIP device" in r.stderr

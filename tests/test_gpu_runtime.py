@@ -38,3 +38,23 @@ def test_zero_ragged(gpu):
     want = a.copy()
     want[3:520] = 0
     assert np.array_equal(got, want)
+
+
+def test_native_cli_runs_gemm_and_matvec():
+    """hb_gemm picks, checks and times a GEMM of each Out mode and a matvec
+    through the C ABI from a native process: one line per shape, the
+    [autotune] log on stderr."""
+    import os
+    import subprocess
+    cli = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))),
+                       "herbert-metal-bf16_amd", "hb_gemm")
+    r = subprocess.run([cli, "--reps", "5", "512x1024x3584", "256x512x768r", "128x256x512f", "mv:4x2560x4608"],
+                       capture_output=True, text=True, timeout=110)
+    assert r.returncode == 0, r.stderr[-2000:]
+    lines = r.stdout.strip().splitlines()
+    assert len(lines) == 4, r.stdout
+    assert lines[0].startswith("512x1024x3584 gemm_") and lines[0].endswith("TFLOP/s")
+    assert lines[1].startswith("256x512x768r gemm_") and "_res" in lines[1]
+    assert lines[2].startswith("128x256x512f gemm_") and "_f32" in lines[2]
+    assert lines[3].startswith("mv:4x2560x4608 matvec_") and lines[3].endswith("GB/s")
+    assert "[autotune] gemm 1024x3584" in r.stderr
