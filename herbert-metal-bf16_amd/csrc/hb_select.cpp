@@ -266,6 +266,11 @@ const Form kMoreForms[] = {
     {"mma_t128x160_s4_o1_b4", 128, 160, 64, 2, 2, 16, 3, 1, 1, 4},
     {"mma_t256x128_w8_s3", 256, 128, 64, 4, 2, 16, 2, 1, 1},
     {"mma_b2", 128, 128, 64, 2, 2, 16, 1, 1, 0, 2},
+    // Small tiles for narrow outputs (the MoE router's 256 columns, the
+    // shared expert): enough tiles to reach every CU.
+    {"mma_t64x128", 64, 128, 64, 2, 2, 16, 2, 1, 1},
+    {"mma_t64x64", 64, 64, 64, 2, 2, 16, 2, 1, 1},
+    {"mma_t32x64", 32, 64, 64, 1, 4, 16, 2, 1, 1},
 };
 // The fused [gate | up] + SwiGLU forms (gate_up_pipes, qwen.rs:2148-2193):
 // bn W rows per tile = bn/2 features.
