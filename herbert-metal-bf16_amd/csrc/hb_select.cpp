@@ -257,6 +257,7 @@ const Form kMoreForms[] = {
     {"mma_t256x192_w8", 256, 192, 64, 4, 2, 32, 1, 1, 1},
     {"mma_t256x192_w8_x16", 256, 192, 64, 4, 2, 16, 1, 1, 1},
     {"mma_t256x192_w8_x16_b4", 256, 192, 64, 4, 2, 16, 1, 1, 1, 4},
+    {"mma_t256_w8_x32_b4", 256, 256, 64, 4, 2, 32, 1, 1, 1, 4},
     {"mma_t128x160", 128, 160, 64, 2, 2, 16, 1, 1, 1},
     {"mma_t128x160_s4", 128, 160, 64, 2, 2, 16, 3, 1, 0},
     {"mma_t128x192_w8_s3", 128, 192, 64, 2, 4, 16, 2, 1, 0},
