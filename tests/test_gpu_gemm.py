@@ -27,6 +27,12 @@ TILES = {
     "t128x160_x16": dict(bm=128, bn=160, bk=64, wm=2, wn=2, mfma=16, dbuf=1, lds_dma=1, order=1),
     "t128x128_band2": dict(bm=128, bn=128, bk=64, wm=2, wn=2, mfma=16, dbuf=1, lds_dma=1, order=0,
                            band=2),
+    "t256x192_w8_x16_b4": dict(bm=256, bn=192, bk=64, wm=4, wn=2, mfma=16, dbuf=1, lds_dma=1, order=1,
+                               band=4),
+    "t256x256_w8_x32_b4": dict(bm=256, bn=256, bk=64, wm=4, wn=2, mfma=32, dbuf=1, lds_dma=1, order=1,
+                               band=4),
+    "t128x160_s4_b4": dict(bm=128, bn=160, bk=64, wm=2, wn=2, mfma=16, dbuf=3, lds_dma=1, order=1, band=4),
+    "t32x64_s3": dict(bm=32, bn=64, bk=64, wm=1, wn=4, mfma=16, dbuf=2, lds_dma=1, order=1),
 }
 
 
