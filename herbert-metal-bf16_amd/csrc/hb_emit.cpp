@@ -117,7 +117,10 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
             }
             if (d.dbuf > 3 || (!d.lds_dma && d.dbuf > 1))
                 return fail(HB_ERR_UNSUPPORTED, "gemm: stages 1..4 (1..2 through registers)");
+            if (d.w_nt > 1 || (d.w_nt && !d.lds_dma))
+                return fail(HB_ERR_UNSUPPORTED, "gemm: w_nt with direct-to-LDS staging");
             std::string band = d.band ? "_b" + std::to_string(d.band) : "";
+            if (d.w_nt) band += "_wnt";
             snprintf(name, sizeof name, "gemm_mma%s_%ux%u_%s%s_t%ux%u_k%u_w%ux%u_x%u_d%u%s_s%u_o%u%s%s",
                      swi ? "_swiglu" : "", d.k, d.n, out_tag(d.out), d.m_first ? "_mf" : "", d.bn,
                      d.bm, d.bk, d.wn, d.wm, d.mfma, d.dbuf, d.lds_dma ? "_dma" : "", shift, d.order,
@@ -133,7 +136,7 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
                           D("HB_STAGES", d.dbuf + 1), D("HB_SWZ", shift),
                           D("HB_ORDER", d.order), D("HB_MFIRST", d.m_first ? 1 : 0),
                           D("HB_DMA", d.lds_dma ? 1 : 0), D("HB_SWIGLU", swi ? 1 : 0),
-                          D("HB_BAND", d.band)};
+                          D("HB_BAND", d.band), D("HB_W_NT", d.w_nt)};
             return HB_OK;
         }
         case HB_KIND_GEMM_SIMT:

@@ -1027,6 +1027,12 @@ int hb_engine_experts(hb_engine* e, uint32_t experts, uint32_t top_k, uint32_t h
             add_gu(ds.m_first ? "mma_swiglu_mf" : "mma_swiglu_nf", ds, false);
         }
         add_gu("mma_swiglu", swi_desc(128), false);
+        {
+            // Each expert's W streamed once: its loads non-temporal.
+            hb_desc d = swi_desc(128);
+            d.w_nt = 1;
+            add_gu("mma_swiglu_wnt", d, false);
+        }
         add_gu("mma_swiglu_n256", swi_desc(256), false);
         if (bm >= 32) add_gu("mma_swiglu_w2x2", swi_desc(128, 2, 2), false);
         add_dn("mma", gemm_desc(inter, hidden, HB_ROWS_SCATTER, bm, 128));
@@ -1036,6 +1042,11 @@ int hb_engine_experts(hb_engine* e, uint32_t experts, uint32_t top_k, uint32_t h
             hb_desc d = gemm_desc(inter, hidden, HB_ROWS_SCATTER, bm, 128);
             d.m_first = !d.m_first;
             add_dn(d.m_first ? "mma_mf" : "mma_nf", d);
+            d.w_nt = 1;
+            add_dn(d.m_first ? "mma_mf_wnt" : "mma_nf_wnt", d);
+            hb_desc d2 = gemm_desc(inter, hidden, HB_ROWS_SCATTER, bm, 128);
+            d2.w_nt = 1;
+            add_dn("mma_wnt", d2);
         }
         if (bm >= 32) add_dn("mma_w2x4_s3", gemm_desc(inter, hidden, HB_ROWS_SCATTER, bm, 128, 2, 4, 2));
         size_t bgu, bdn;

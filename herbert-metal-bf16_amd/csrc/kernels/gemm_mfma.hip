@@ -106,6 +106,12 @@ HB_DEV u32 lpos(u32 r, u32 c) { return r * CH + (c ^ ((r >> HB_SWZ) & (CH - 1)))
 #ifndef HB_PROBE_SKIP
 #define HB_PROBE_SKIP 0
 #endif
+// HB_W_NT 1: W's direct-to-LDS loads non-temporal (W read by one tile).
+#if defined(HB_W_NT) && HB_W_NT
+#define HB_W_CPOL " nt"
+#else
+#define HB_W_CPOL ""
+#endif
 
 HB_DEV acc_t mfma(bf16x8 a, bf16x8 b, acc_t c) {
 #if HB_PROBE_SKIP & 2
@@ -353,7 +359,7 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
                          :: "s"(lds_addr(&sX[q * NT + wave * 64])), "v"(xoff[q] * 2), "s"(rX),
                             "s"(kb) : "memory");
         else
-            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+            asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen" HB_W_CPOL " lds"
                          :: "s"(lds_addr(&sW[(q - X_LD) * NT + wave * 64])),
                             "v"(woff[q - X_LD] * 2), "s"(rW), "s"(kb) : "memory");
     };

@@ -106,12 +106,12 @@ class Range(ctypes.Structure):
 _DESC_FIELDS = ["kind", "k", "n", "out", "rows_of", "m_first", "bm", "bn", "bk", "wm", "wn",
                 "mfma", "dbuf", "swz", "order", "mv_m", "split", "persist", "rows", "form",
                 "top_k", "experts", "tiles", "rows_max", "lds_dma", "unroll", "band", "xsrc", "eps_bits", "plus_one",
-                "x_lds"]
+                "x_lds", "w_nt"]
 
 
 class Desc(ctypes.Structure):
     """hb_desc: a kernel's shape-keyed descriptor (what an emitter fixes)."""
-    _fields_ = [(f, ctypes.c_uint32) for f in _DESC_FIELDS] + [("reserved", ctypes.c_uint32)]
+    _fields_ = [(f, ctypes.c_uint32) for f in _DESC_FIELDS]
 
     def __init__(self, **kw):
         super().__init__()
