@@ -1047,6 +1047,13 @@ int hb_engine_experts(hb_engine* e, uint32_t experts, uint32_t top_k, uint32_t h
             hb_desc d2 = gemm_desc(inter, hidden, HB_ROWS_SCATTER, bm, 128);
             d2.w_nt = 1;
             add_dn("mma_wnt", d2);
+            if (bm >= 32) {
+                // 256-wide W tiles, 8 waves, 3 stages, in the same order.
+                hb_desc d3 = gemm_desc(inter, hidden, HB_ROWS_SCATTER, bm, 256, 2, 4, 2);
+                d3.m_first = d.m_first;
+                d3.w_nt = 1;
+                add_dn(d3.m_first ? "mma_n256_w8_s3_mf_wnt" : "mma_n256_w8_s3_nf_wnt", d3);
+            }
         }
         if (bm >= 32) add_dn("mma_w2x4_s3", gemm_desc(inter, hidden, HB_ROWS_SCATTER, bm, 128, 2, 4, 2));
         size_t bgu, bdn;
