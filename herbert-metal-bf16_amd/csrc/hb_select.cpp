@@ -1052,6 +1052,7 @@ int hb_engine_experts(hb_engine* e, uint32_t experts, uint32_t top_k, uint32_t h
                 hb_desc d3 = gemm_desc(inter, hidden, HB_ROWS_SCATTER, bm, 256, 2, 4, 2);
                 d3.m_first = d.m_first;
                 d3.w_nt = 1;
+                d3.order = 1;  // each XCD a contiguous share of the table's tiles
                 add_dn(d3.m_first ? "mma_n256_w8_s3_mf_wnt" : "mma_n256_w8_s3_nf_wnt", d3);
             }
         }

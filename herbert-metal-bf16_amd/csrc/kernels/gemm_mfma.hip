@@ -177,7 +177,16 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     const u32 wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar
     const u32 wm = wave % WM, wn = wave / WM;
     u32 g = blockIdx.x;
-    if (HB_ORDER == 1) g = xcd_remap(g, gridDim.x);
+    if constexpr (HB_ORDER == 1 && ROWS != 0) {
+        // Experts: only the table's tiles[0] row tiles are real, so the XCD
+        // ranges split those (total groups), not the launch: XCD x takes
+        // groups x*per .. x*per + per - 1; the rest of its groups return.
+        const u32 total = tiles[0] * NTILES, per = (total + 7) / 8;
+        const u32 i = g >> 3;
+        g = i < per ? (g & 7u) * per + i : 0xffffffffu;
+    } else if (HB_ORDER == 1) {
+        g = xcd_remap(g, gridDim.x);
+    }
 
     // The tile: its first row (dense row or sorted pair), its rows, its
     // column tile and its expert.
@@ -208,7 +217,10 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
         row0 = gm * BM;
         rows = m - row0 < BM ? m - row0 : BM;
     } else {
-        const u32 tmax = gridDim.x / NTILES;
+        // The row-tile count walked: the table's (XCD-balanced order) or the
+        // launch's.
+        const u32 tmax = HB_ORDER == 1 ? tiles[0] : gridDim.x / NTILES;
+        if (g == 0xffffffffu || tmax == 0) return;
         u32 t;
         if (HB_MFIRST) { t = g % tmax; gn = g / tmax; }
         else { gn = g % NTILES; t = g / NTILES; }

@@ -153,14 +153,15 @@ EXPERT_TILES = {
     "m16_dma_nf": dict(wm=1, wn=4, mfma=16, bn=128, bk=64, dbuf=1, lds_dma=1, m_first=False),
     "m128_wnt_nf": dict(wm=1, wn=4, mfma=16, bn=128, bk=64, dbuf=1, lds_dma=1, m_first=False, w_nt=1),
     "m128_n256_w8_s3_nf_wnt": dict(wm=2, wn=4, mfma=16, bn=256, bk=64, dbuf=2, lds_dma=1, m_first=False,
-                                   w_nt=1),
+                                   w_nt=1, order=1),
+    "m32_mf_o1": dict(wm=1, wn=4, mfma=16, bn=128, bk=64, dbuf=1, lds_dma=1, order=1),
 }
 
 
 @pytest.mark.parametrize("tname,bm", [("m16_reg", 16), ("m32_reg_d", 32), ("m64_dma", 64),
                                       ("m16_dma", 16), ("m128_w2x2", 128), ("m64_w2x4_s3", 64),
                                       ("m16_dma_nf", 16), ("m128_wnt_nf", 128),
-                                      ("m128_n256_w8_s3_nf_wnt", 128)])
+                                      ("m128_n256_w8_s3_nf_wnt", 128), ("m32_mf_o1", 32)])
 def test_grouped_gemm_gather_and_scatter(gpu, tname, bm):
     """Config 5's grouped gate|up (Gather: sorted row p reads X row
     list[p]/top_k) and down (Scatter: writes row list[p]), on 512 tokens
