@@ -259,3 +259,22 @@ def test_time_each_brackets_every_launch(gpu):
         gpu.free(b)
     assert abs(sum(each) * 7 - total) <= 1e-3 * total + 1e-6
     assert each[1] > 4 * each[0] > 0
+
+
+def test_descriptor_refusals(gpu):
+    """Fields a kernel cannot honour are refused at build, naming the rule:
+    w_nt without direct-to-LDS staging, x_lds past 64 KiB of x (or on the
+    MFMA matvec), a combine of more than 16 slots."""
+    with pytest.raises(hb.HerbertError, match="w_nt"):
+        gpu.pipeline(hb.gemm_mma(256, 512, 0, bm=128, bn=128, bk=64, wm=2, wn=2, mfma=16, dbuf=1,
+                                 lds_dma=0, w_nt=1))
+    with pytest.raises(hb.HerbertError, match="x_lds"):
+        gpu.pipeline(hb.matvec(9216, 2560, 0, mv_m=8, rows=2, form=2, x_lds=True))
+    with pytest.raises(hb.HerbertError, match="x_lds"):
+        gpu.pipeline(hb.matvec(2560, 4608, 0, mv_m=4, form=1, x_lds=True))
+    with pytest.raises(hb.HerbertError, match="top_k"):
+        gpu.pipeline(hb.Desc(kind=hb.Kind.COMBINE, n=2048, top_k=17))
+    assert gpu.kernel_kind(-1) == 0
+    k = gpu.pipeline(hb.gemm_mma(256, 512, 0, bm=128, bn=128, bk=64, wm=2, wn=2, mfma=16, dbuf=1,
+                                 lds_dma=1, w_nt=1))
+    assert gpu.kernel_kind(k) == hb.Kind.GEMM and gpu.kernel_name(k).find("_wnt") > 0
