@@ -59,6 +59,7 @@ hb_desc with_defaults(const hb_desc& in) {
         if (!d.rows) d.rows = 4;
         if (!d.unroll) d.unroll = 4;
         if (d.form == 1) d.rows = 16;
+        if (!d.mv_waves) d.mv_waves = 4;
     }
     return d;
 }
@@ -174,8 +175,14 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
                 return fail(HB_ERR_UNSUPPORTED, "matvec Out::Swiglu: even rows (gate and up) and n");
             if (d.xsrc == HB_XSRC_NORM && ((uint64_t)d.mv_m * d.k * 2 > 65536 || d.k % 256))
                 return fail(HB_ERR_UNSUPPORTED, "matvec XSrc::Norm: m*k*2 <= 64 KiB of LDS, k a multiple of 256");
-            if (d.x_lds > 1 || (d.x_lds && (d.form == 1 || (uint64_t)d.mv_m * d.k * 2 > 65536)))
-                return fail(HB_ERR_UNSUPPORTED, "matvec x_lds: VALU forms, m*k*2 <= 64 KiB of LDS");
+            if (d.mv_waves != 4 && d.mv_waves != 8 && d.mv_waves != 16)
+                return fail(HB_ERR_UNSUPPORTED, "matvec: mv_waves 4, 8 or 16");
+            if (d.mv_waves != 4 && d.xsrc == HB_XSRC_NORM)
+                return fail(HB_ERR_UNSUPPORTED, "matvec XSrc::Norm: 4 waves");
+            if (d.x_lds > 1 ||
+                (d.x_lds && (d.form == 1 || (uint64_t)d.mv_m * d.k * 2 > (d.mv_waves == 4 ? 65536u : 147456u))))
+                return fail(HB_ERR_UNSUPPORTED,
+                            "matvec x_lds: VALU forms, m*k*2 <= 64 KiB of LDS (144 KiB with 8 or 16 waves)");
             const bool xl = d.x_lds && d.xsrc != HB_XSRC_NORM;
             if (!d.k || !d.n || d.k % (8 * d.split) || (d.split != 1 && d.split != 2 && d.split != 4))
                 return fail(HB_ERR_UNSUPPORTED, "matvec: K a multiple of 8*split, split 1, 2 or 4");
@@ -190,6 +197,7 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
             if (d.xsrc == HB_XSRC_NORM)
                 snprintf(xtag, sizeof xtag, "_nrm%08x%s", d.eps_bits, d.plus_one ? "p1" : "");
             if (xl) strncat(xtag, "_xl", sizeof xtag - strlen(xtag) - 1);
+            if (d.mv_waves != 4) strncat(xtag, d.mv_waves == 8 ? "_w8" : "_w16", sizeof xtag - strlen(xtag) - 1);
             snprintf(name, sizeof name, "matvec_%ux%u%s%s_r%u_k%u%s_m%u_%s_u%u", d.k, d.n, xtag,
                      d.out == HB_OUT_F32 ? "_f32" : d.out == HB_OUT_RESIDUAL ? "_res"
                                                   : d.out == HB_OUT_SWIGLU ? "_sw" : "",
@@ -197,13 +205,13 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
                      d.mv_m, d.form == 1 ? "mfma" : d.form == 2 ? "dot2" : "valu", d.unroll);
             e->name = name;
             e->source = "matvec.hip";
-            e->threads = 256;
+            e->threads = 64 * d.mv_waves;
             e->nbind = d.xsrc == HB_XSRC_NORM ? 4 : 3;
             e->defines = {D("HB_K", d.k),         D("HB_N", d.n),          D("HB_OUT", d.out),
                           D("HB_MV_M", d.mv_m),   D("HB_FORM", d.form),    D("HB_ROWS", d.rows),
                           D("HB_SPLIT", d.split), D("HB_PERSIST", d.persist), D("HB_UNROLL", d.unroll),
                           D("HB_XSRC", d.xsrc),   D("HB_EPS", d.eps_bits), D("HB_PLUS1", d.plus_one),
-                          D("HB_XLDS", xl ? 1 : 0)};
+                          D("HB_XLDS", xl ? 1 : 0), D("HB_WAVES", d.mv_waves)};
             return HB_OK;
         }
         case HB_KIND_ROUTE:
@@ -329,7 +337,7 @@ uint32_t groups_of(const hb_desc& d, uint32_t m) {
             return cdiv(m, bm) * nt;                                 // gemm_mma_groups
         }
         case HB_KIND_MATVEC: {  // matvec_groups / matvec_split_groups / matvec_full_groups
-            uint32_t rb = d.form == 1 ? 16 : d.rows, per = 4 / d.split;
+            uint32_t rb = d.form == 1 ? 16 : d.rows, per = d.mv_waves / d.split;
             uint32_t n = d.n;
             if (d.out == HB_OUT_SWIGLU) n /= 2, rb /= 2;  // output rows: gate rows
             uint32_t wgs = cdiv(cdiv(n, rb), per);

@@ -861,6 +861,25 @@ int hb_engine_matvec_fused(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, u
                 dx.x_lds = 1;
                 add((mv_m > 1 ? "d" : "r") + std::to_string(rows) + (p ? "p" + std::to_string(p) : "") + "u8xl", dx);
             }
+    // For several rows, x staged once per CU by one 16-wave workgroup (or
+    // two 8-wave ones) with up to 144 KiB of LDS: the long-K o and down
+    // shapes, whose x the 4-wave workgroups cannot hold or would stage per
+    // four waves (measured at m=8: down 2.6 -> 3.5 TB/s, o 2.1 -> 2.5).
+    if (mv_m > 1 && xsrc != HB_XSRC_NORM && (uint64_t)mv_m * k * 2 <= 147456) {
+        const bool small = (uint64_t)mv_m * k * 2 <= 65536;
+        const uint32_t r1 = out == HB_OUT_SWIGLU ? 2 : 1;
+        struct W { uint32_t waves, rows, persist, unroll; };
+        for (W w : {W{16, r1, 0, 8}, W{16, r1, 256, 4}, W{16, r1, 256, 8}, W{8, 2, 256, 4}}) {
+            if (!small && w.persist != 256) continue;  // one workgroup per CU
+            if (w.rows * mv_m > 64) continue;
+            hb_desc dw = desc(2, w.rows, 1, w.persist);
+            dw.unroll = w.unroll;
+            dw.x_lds = 1;
+            dw.mv_waves = w.waves;
+            add("d" + std::to_string(w.rows) + (w.persist ? "p" + std::to_string(w.persist) : "") + "u" +
+                    std::to_string(w.unroll) + "xl_w" + std::to_string(w.waves), dw);
+        }
+    }
     for (uint32_t split : splits)
         for (uint32_t p : pers) {
             if (fused) break;  // the fusions are VALU forms

@@ -40,14 +40,19 @@
 // bf16-rounded sums, N/2 wide.
 //
 // Constants: HB_K, HB_N, HB_OUT, HB_MV_M, HB_FORM, HB_ROWS (form 0),
-// HB_SPLIT, HB_PERSIST, HB_UNROLL, HB_XSRC, HB_EPS, HB_PLUS1.  Bindings: W,
+// HB_SPLIT, HB_PERSIST, HB_UNROLL, HB_XSRC, HB_EPS, HB_PLUS1, HB_XLDS,
+// HB_WAVES (wavefronts per workgroup: 4, 8 or 16).  Bindings: W,
 // x, y[, norm weights]; then m (<= MV_M).
 #include "hb_common.h"
 
 constexpr u32 K = HB_K, N = HB_N, MV = HB_MV_M;
 constexpr int OUT = HB_OUT;
 constexpr u32 SPLIT = HB_SPLIT, U = HB_UNROLL;
-constexpr u32 WAVES = 4, NT = 256;
+#ifndef HB_WAVES
+#define HB_WAVES 4
+#endif
+constexpr u32 WAVES = HB_WAVES, NT = 64 * WAVES;
+static_assert(WAVES == 4 || WAVES == 8 || WAVES == 16, "4, 8 or 16 waves");
 constexpr u32 GROUPS_PER_WG = WAVES / SPLIT;  // row blocks per workgroup
 #if HB_FORM != 1
 constexpr u32 RB = HB_ROWS;                   // rows per row block
@@ -82,7 +87,9 @@ constexpr u32 NBLK = (NOUT + RO - 1) / RO;
 constexpr u32 KS = K / SPLIT;                 // K of one wave's range
 static_assert(!SWO || (RB % 2 == 0 && N % 2 == 0 && HB_FORM != 1), "Out::Swiglu: VALU forms, even rows");
 static_assert(HB_XSRC == 0 || HB_FORM != 1, "XSrc fusions: VALU forms");
-static_assert(!HB_XIN_LDS || (HB_FORM != 1 && MV * K * 2 <= 65536), "x in LDS: VALU forms, m*K*2 <= 64 KiB");
+static_assert(HB_XSRC != 2 || WAVES == 4, "XSrc::Norm: 4 waves");
+static_assert(!HB_XIN_LDS || (HB_FORM != 1 && MV * K * 2 <= (WAVES == 4 ? 65536u : 147456u)),
+              "x in LDS: VALU forms, m*K*2 <= 64 KiB (144 KiB with 8 or 16 waves)");
 
 static_assert(WAVES % SPLIT == 0, "split divides the waves");
 static_assert(K % (8 * SPLIT) == 0 && KS % 8 == 0, "K split in whole chunks");

@@ -106,7 +106,7 @@ class Range(ctypes.Structure):
 _DESC_FIELDS = ["kind", "k", "n", "out", "rows_of", "m_first", "bm", "bn", "bk", "wm", "wn",
                 "mfma", "dbuf", "swz", "order", "mv_m", "split", "persist", "rows", "form",
                 "top_k", "experts", "tiles", "rows_max", "lds_dma", "unroll", "band", "xsrc", "eps_bits", "plus_one",
-                "x_lds", "w_nt"]
+                "x_lds", "w_nt", "mv_waves"]
 
 
 class Desc(ctypes.Structure):
@@ -274,16 +274,17 @@ def swiglu_rows(nf):
 
 
 def matvec(kdim, n, out, mv_m=1, rows=4, split=1, persist=0, form=0, unroll=4, xsrc=0, eps=0.0,
-           plus_one=False, x_lds=False):
+           plus_one=False, x_lds=False, waves=0):
     """matvec / matvec_split (kernels.rs:146, 502, 640): y[m][n] = x[m][k].W^T for m <= mv_m;
     form 0 the VALU layout (rows per wave), 1 the MFMA layout (16 rows per wave), 2 the VALU
     layout with v_dot2; xsrc / out Swiglu the decode fusions (VALU forms); x_lds the x rows
-    staged in LDS once per workgroup (VALU forms)."""
+    staged in LDS once per workgroup (VALU forms); waves: wavefronts per workgroup (0 = 4, 8, 16;
+    with x_lds up to 144 KiB of x)."""
     import struct
     eps_bits = struct.unpack("<I", struct.pack("<f", eps))[0]
     return Desc(kind=Kind.MATVEC, k=kdim, n=n, out=out, mv_m=mv_m, rows=rows, split=split,
                 persist=persist, form=form, unroll=unroll, xsrc=xsrc, eps_bits=eps_bits,
-                plus_one=1 if plus_one else 0, x_lds=1 if x_lds else 0)
+                plus_one=1 if plus_one else 0, x_lds=1 if x_lds else 0, mv_waves=waves)
 
 
 class Gpu:

@@ -154,6 +154,11 @@ typedef struct hb_desc {
      * W read by one tile only (the experts' weights): measured +6-8% on the
      * grouped GEMMs, slower where tiles share W through L2. */
     uint32_t w_nt;
+    /* matvec (plain x or XSrc::Swiglu): wavefronts per workgroup, 0 or 4
+     * (256 threads), 8 or 16.  With x_lds, 8 and 16 waves stage up to
+     * 144 KiB of x (one workgroup per CU, x staged once per CU), against
+     * 64 KiB for 4. */
+    uint32_t mv_waves;
 } hb_desc;
 
 /* Gpu::pipeline(&Emitted) (metal/gpu.rs:127-148) for the kernel the

@@ -208,6 +208,53 @@ def test_matvec_x_in_lds(gpu, name, k, n, out, form, m):
     check_close(got, want, k, abs_products(x, w), "%s %s xl m=%d" % (name, form, m), acc=acc)
 
 
+WAVE_FORMS = {"w16_r1_p256_u4": dict(waves=16, rows=1, persist=256, unroll=4),
+              "w16_r1_u8": dict(waves=16, rows=1, unroll=8),
+              "w8_r2_p256_u4": dict(waves=8, rows=2, persist=256, unroll=4)}
+
+
+@pytest.mark.parametrize("m", [3, 8])
+@pytest.mark.parametrize("form", sorted(WAVE_FORMS))
+@pytest.mark.parametrize("name,k,n,out", [SHAPES[0], SHAPES[1], SHAPES[3]])
+def test_matvec_x_in_lds_waves(gpu, name, k, n, out, form, m):
+    """x staged in LDS by 8- and 16-wave workgroups (down at 8 rows: 144 KiB):
+    bit-equal to the 4-wave form reading x from memory (each row's sum is one
+    wave's in the same order), within the contract of the oracle; m=3 on a
+    kernel built for 8 rows."""
+    f = dict(WAVE_FORMS[form], form=2, split=1)
+    if 8 * k * 2 > 65536 and not f.get("persist"):
+        pytest.skip("past 64 KiB of x: one workgroup per CU (persistent)")
+    x = hb.normal_bf16(0x5EED0031, 1.0, (m, k))
+    w = hb.normal_bf16(0x5EED0032, 0.02, (n, k))
+    y0 = hb.normal_bf16(23, 1.0, (m, n)) if out == 2 else None
+    got = run_mv(gpu, x, w, out, y0, x_lds=True, **f)
+    ref = run_mv(gpu, x, w, out, y0, form=2, split=1, rows=f["rows"], unroll=f["unroll"])
+    assert np.array_equal(got, ref), "%s %s m=%d: 8/16-wave x in LDS differs" % (name, form, m)
+    acc = orc.gemm(x, w, orc.OUT_F32) if out == 2 else None
+    check_close(got, orc.gemm(x, w, out, y0), k, abs_products(x, w), "%s %s m=%d" % (name, form, m), acc=acc)
+
+
+def test_matvec_waves_fusions(gpu):
+    """XSrc::Swiglu (down, 8 rows: the swiglu'd x, 144 KiB, in LDS) and
+    Out::Swiglu with 16-wave workgroups: bit-equal to the 4-wave forms
+    reading x from memory."""
+    m, k, n = 8, 9216, 2560
+    gu = hb.normal_bf16(0x5EED0033, 1.0, (m, 2 * k))
+    w = hb.normal_bf16(0x5EED0034, 0.02, (n, k))
+    y0 = hb.normal_bf16(25, 1.0, (m, n))
+    f = dict(form=2, rows=2, split=1, unroll=4)
+    got = run_mv_fused(gpu, gu, w, hb.Out.Residual, y0, m, xsrc=hb.XSrc.Swiglu, x_lds=True, waves=16,
+                       persist=256, **f)
+    ref = run_mv_fused(gpu, gu, w, hb.Out.Residual, y0, m, xsrc=hb.XSrc.Swiglu, **f)
+    assert np.array_equal(got, ref), "XSrc::Swiglu: 16-wave x in LDS differs from x from memory"
+    k2, nf = 2560, 9216
+    x = hb.normal_bf16(0x5EED0035, 1.0, (m, k2))
+    w2 = hb.normal_bf16(0x5EED0036, 0.02, (2 * nf, k2))
+    got = run_mv_fused(gpu, x, w2, hb.Out.Swiglu, None, m, x_lds=True, waves=16, **f)
+    ref = run_mv_fused(gpu, x, w2, hb.Out.Swiglu, None, m, **f)
+    assert np.array_equal(got, ref), "Out::Swiglu: 16-wave x in LDS differs from x from memory"
+
+
 @pytest.mark.parametrize("m", [1, 2])
 def test_matvec_x_in_lds_fusions(gpu, m):
     """XSrc::Swiglu with the swiglu'd x staged in LDS (down, K=9216, built for
