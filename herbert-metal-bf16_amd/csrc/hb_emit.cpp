@@ -58,7 +58,7 @@ hb_desc with_defaults(const hb_desc& in) {
         if (!d.split) d.split = 1;
         if (!d.rows) d.rows = 4;
         if (!d.unroll) d.unroll = 4;
-        if (d.form == 1) d.rows = 16;
+        if (d.form == 1 || d.form == 3) d.rows = 16;
         if (!d.mv_waves) d.mv_waves = 4;
     }
     return d;
@@ -167,9 +167,10 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
                           D("HB_BN", d.bn), D("HB_MFIRST", d.m_first ? 1 : 0)};
             return HB_OK;
         case HB_KIND_MATVEC: {
-            if (d.out > HB_OUT_SWIGLU || d.form > 2 || d.xsrc > HB_XSRC_NORM)
+            if (d.out > HB_OUT_SWIGLU || d.form > 3 || d.xsrc > HB_XSRC_NORM)
                 return fail(HB_ERR_INVALID, "matvec: out / form / xsrc out of range");
-            if ((d.xsrc || d.out == HB_OUT_SWIGLU) && d.form == 1)
+            const bool mma = d.form == 1 || d.form == 3;
+            if ((d.xsrc || d.out == HB_OUT_SWIGLU) && mma)
                 return fail(HB_ERR_UNSUPPORTED, "matvec: XSrc and Out::Swiglu fusions in the VALU forms");
             if (d.out == HB_OUT_SWIGLU && (d.rows % 2 || d.n % 2))
                 return fail(HB_ERR_UNSUPPORTED, "matvec Out::Swiglu: even rows (gate and up) and n");
@@ -180,17 +181,19 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
             if (d.mv_waves != 4 && d.xsrc == HB_XSRC_NORM)
                 return fail(HB_ERR_UNSUPPORTED, "matvec XSrc::Norm: 4 waves");
             if (d.x_lds > 1 ||
-                (d.x_lds && (d.form == 1 || (uint64_t)d.mv_m * d.k * 2 > (d.mv_waves == 4 ? 65536u : 147456u))))
+                (d.x_lds && (mma || (uint64_t)d.mv_m * d.k * 2 > (d.mv_waves == 4 ? 65536u : 147456u))))
                 return fail(HB_ERR_UNSUPPORTED,
                             "matvec x_lds: VALU forms, m*k*2 <= 64 KiB of LDS (144 KiB with 8 or 16 waves)");
             const bool xl = d.x_lds && d.xsrc != HB_XSRC_NORM;
             if (!d.k || !d.n || d.k % (8 * d.split) || (d.split != 1 && d.split != 2 && d.split != 4))
                 return fail(HB_ERR_UNSUPPORTED, "matvec: K a multiple of 8*split, split 1, 2 or 4");
-            if (d.form != 1 && (d.rows > 8 || !d.rows || d.rows * d.mv_m > 64 || d.mv_m > 16))
+            if (!mma && (d.rows > 8 || !d.rows || d.rows * d.mv_m > 64 || d.mv_m > 16))
                 return fail(HB_ERR_UNSUPPORTED, "matvec: rows 1..8, rows*m <= 64");
-            if (d.form == 1 && (d.mv_m > 16 || (d.k / d.split) % 32))
+            if (mma && (d.mv_m > 16 || (d.k / d.split) % 32))
                 return fail(HB_ERR_UNSUPPORTED, "matvec (MFMA): m <= 16, K/split a multiple of 32");
-            if (!d.unroll || d.unroll > (d.form == 1 ? 16u : 8u))
+            if (d.form == 3 && ((d.unroll != 4 && d.unroll != 8 && d.unroll != 16) || d.mv_waves * d.unroll > 64))
+                return fail(HB_ERR_UNSUPPORTED, "matvec (MFMA, W through LDS): unroll 4, 8 or 16, waves*unroll <= 64");
+            if (!d.unroll || d.unroll > (mma ? 16u : 8u))
                 return fail(HB_ERR_UNSUPPORTED, "matvec: unroll 1..8 (MFMA form 1..16)");
             char xtag[48] = "";
             if (d.xsrc == HB_XSRC_SWIGLU) snprintf(xtag, sizeof xtag, "_swi");
@@ -202,7 +205,7 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
                      d.out == HB_OUT_F32 ? "_f32" : d.out == HB_OUT_RESIDUAL ? "_res"
                                                   : d.out == HB_OUT_SWIGLU ? "_sw" : "",
                      d.rows, d.split, d.persist ? ("_p" + std::to_string(d.persist)).c_str() : "",
-                     d.mv_m, d.form == 1 ? "mfma" : d.form == 2 ? "dot2" : "valu", d.unroll);
+                     d.mv_m, d.form == 1 ? "mfma" : d.form == 2 ? "dot2" : d.form == 3 ? "mfl" : "valu", d.unroll);
             e->name = name;
             e->source = "matvec.hip";
             e->threads = 64 * d.mv_waves;
@@ -337,7 +340,7 @@ uint32_t groups_of(const hb_desc& d, uint32_t m) {
             return cdiv(m, bm) * nt;                                 // gemm_mma_groups
         }
         case HB_KIND_MATVEC: {  // matvec_groups / matvec_split_groups / matvec_full_groups
-            uint32_t rb = d.form == 1 ? 16 : d.rows, per = d.mv_waves / d.split;
+            uint32_t rb = d.form == 1 || d.form == 3 ? 16 : d.rows, per = d.mv_waves / d.split;
             uint32_t n = d.n;
             if (d.out == HB_OUT_SWIGLU) n /= 2, rb /= 2;  // output rows: gate rows
             uint32_t wgs = cdiv(cdiv(n, rb), per);

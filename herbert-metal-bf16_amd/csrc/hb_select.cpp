@@ -880,6 +880,18 @@ int hb_engine_matvec_fused(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, u
                     std::to_string(w.unroll) + "xl_w" + std::to_string(w.waves), dw);
         }
     }
+    // The MFMA arithmetic with W read in row order through a wave-private
+    // LDS tile (form 3): for several rows, where the VALU forms run out of
+    // issue (measured at m=8: gate_up 4.4 -> 5.0 TB/s, lm_head 5.3 -> 6.1).
+    if (mv_m > 1 && !fused && k % 128 == 0) {
+        struct F { uint32_t unroll, split, persist; };
+        for (F f : {F{4, 4, 0}, F{4, 2, 0}, F{4, 1, 512}, F{4, 4, 512}, F{8, 2, 0}, F{8, 4, 0}, F{8, 4, 512}}) {
+            hb_desc d3 = desc(3, 16, f.split, f.persist);
+            d3.unroll = f.unroll;
+            add("mfl_u" + std::to_string(f.unroll) + "k" + std::to_string(f.split) +
+                    (f.persist ? "p" + std::to_string(f.persist) : ""), d3);
+        }
+    }
     for (uint32_t split : splits)
         for (uint32_t p : pers) {
             if (fused) break;  // the fusions are VALU forms

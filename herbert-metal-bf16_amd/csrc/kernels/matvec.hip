@@ -9,7 +9,7 @@
 // (store).  The reference decodes one row; m up to MV_M is this build's
 // extension (one W read serves every row).
 //
-// Three forms (HB_FORM):
+// Four forms (HB_FORM):
 //  0 (VALU, the reference's arithmetic layout): a wavefront computes ROWS
 //    consecutive rows of W over its K range; lane l takes the 16-byte
 //    chunks l, l+64, ... of it, UNROLL chunks per row in flight; then a
@@ -27,6 +27,10 @@
 //    64-byte segments) and a block 64*UNROLL bytes of each row; x uses the
 //    same K mapping.
 //    Up to 4 independent accumulators, summed at the end.
+//  3 (MFMA, W through LDS): form 1's MFMAs and x, with W loaded in row
+//    order (512 B or 1 KB of one row per load instruction, as the VALU
+//    forms read it) and turned into the A operand through a wave-private
+//    LDS tile: the MFMA's arithmetic with the VALU forms' HBM access.
 // Both: SPLIT wavefronts of a workgroup share a row block's K (contiguous
 // ranges); their partials are added in wave order through LDS.  PERSIST
 // > 0: that many workgroups loop over the row blocks.
@@ -45,6 +49,9 @@
 // x, y[, norm weights]; then m (<= MV_M).
 #include "hb_common.h"
 
+// The MFMA forms: 1 (W loaded as the A operand) and 3 (W through LDS).
+#define HB_MMA (HB_FORM == 1 || HB_FORM == 3)
+
 constexpr u32 K = HB_K, N = HB_N, MV = HB_MV_M;
 constexpr int OUT = HB_OUT;
 constexpr u32 SPLIT = HB_SPLIT, U = HB_UNROLL;
@@ -54,13 +61,16 @@ constexpr u32 SPLIT = HB_SPLIT, U = HB_UNROLL;
 constexpr u32 WAVES = HB_WAVES, NT = 64 * WAVES;
 static_assert(WAVES == 4 || WAVES == 8 || WAVES == 16, "4, 8 or 16 waves");
 constexpr u32 GROUPS_PER_WG = WAVES / SPLIT;  // row blocks per workgroup
-#if HB_FORM != 1
+#if !HB_MMA
 constexpr u32 RB = HB_ROWS;                   // rows per row block
 #else
 constexpr u32 RB = 16;
 #endif
 #ifndef HB_XSRC
 #define HB_XSRC 0
+#endif
+#ifndef HB_PROBE_NOW
+#define HB_PROBE_NOW 0
 #endif
 #ifndef HB_PROBE_NOX
 #define HB_PROBE_NOX 0
@@ -85,15 +95,15 @@ constexpr u32 NOUT = SWO ? N / 2 : N;         // output rows
 constexpr u32 RO = SWO ? RB / 2 : RB;         // output rows per row block
 constexpr u32 NBLK = (NOUT + RO - 1) / RO;
 constexpr u32 KS = K / SPLIT;                 // K of one wave's range
-static_assert(!SWO || (RB % 2 == 0 && N % 2 == 0 && HB_FORM != 1), "Out::Swiglu: VALU forms, even rows");
-static_assert(HB_XSRC == 0 || HB_FORM != 1, "XSrc fusions: VALU forms");
+static_assert(!SWO || (RB % 2 == 0 && N % 2 == 0 && !HB_MMA), "Out::Swiglu: VALU forms, even rows");
+static_assert(HB_XSRC == 0 || !HB_MMA, "XSrc fusions: VALU forms");
 static_assert(HB_XSRC != 2 || WAVES == 4, "XSrc::Norm: 4 waves");
-static_assert(!HB_XIN_LDS || (HB_FORM != 1 && MV * K * 2 <= (WAVES == 4 ? 65536u : 147456u)),
+static_assert(!HB_XIN_LDS || (!HB_MMA && MV * K * 2 <= (WAVES == 4 ? 65536u : 147456u)),
               "x in LDS: VALU forms, m*K*2 <= 64 KiB (144 KiB with 8 or 16 waves)");
 
 static_assert(WAVES % SPLIT == 0, "split divides the waves");
 static_assert(K % (8 * SPLIT) == 0 && KS % 8 == 0, "K split in whole chunks");
-static_assert(HB_FORM != 1 || (MV <= 16 && KS % 32 == 0), "MFMA form: m <= 16, K steps of 32");
+static_assert(!HB_MMA || (MV <= 16 && KS % 32 == 0), "MFMA form: m <= 16, K steps of 32");
 
 // bf16(g * sigmoid(g) * u) as f32: swiglu's arithmetic (the SwiGLU kernels'
 // own expression, kernels.rs:256-261).
@@ -129,6 +139,10 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
 #endif
                                                            u32 m_launch) {
     __shared__ float part[SPLIT > 1 ? WAVES * RB * 16 : 1];
+#if HB_FORM == 3
+    static_assert((U == 4 || U == 8 || U == 16) && WAVES * U <= 64, "W through LDS: unroll 4, 8 or 16, WAVES*U KiB of tile");
+    __shared__ u32x4 wtile[WAVES * 16 * 4 * U];
+#endif
     const u32 tid = threadIdx.x, lane = tid & 63u;
     const u32 wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const u32 gi = wave / SPLIT, sp = wave % SPLIT;  // row block in the group, K part
@@ -210,7 +224,7 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
     // plain x, or a prologue a persistent workgroup amortises, lost 1-15%).
     // The MFMA form reads x from memory.
     constexpr bool HOIST = HB_XSRC == 2 && HB_PERSIST == 0;
-    bool pending = HB_XIN_LDS && HB_FORM != 1 && HOIST;
+    bool pending = HB_XIN_LDS && !HB_MMA && HOIST;
 #if HB_XIN_LDS
     if constexpr (!HOIST) prologue();
 #endif
@@ -228,7 +242,7 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
     for (u32 wg = blockIdx.x; wg < nwg; wg += step) {
         const u32 blk = wg * GROUPS_PER_WG + gi;
         const u32 n0 = blk * RO;  // first output row
-#if HB_FORM != 1
+#if !HB_MMA
         // ---- VALU: ROWS rows, lanes over 16-byte chunks ----
         float acc[RB][MV];
 #pragma unroll
@@ -259,8 +273,12 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
                 const bool on = decltype(full)::value || (u * 64 + 64 <= REM) || (c0 + 64 * u < CHUNKS);
 #pragma unroll
                 for (u32 r = 0; r < RB; r++)
+#if HB_PROBE_NOW  // development probe: no W loads (wrong results)
+                    wv[u][r] = u32x4{lane + c0, u + r, lane ^ c0, (u32)(u64)wr[r]};
+#else
                     wv[u][r] = on ? __builtin_nontemporal_load((const u32x4*)(wr[r] + k0 + (c0 + 64 * u) * 8))
                                   : u32x4{0u, 0u, 0u, 0u};
+#endif
             }
 #if HB_XIN_LDS
             if (HOIST && pending) {
@@ -287,6 +305,32 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
                     xs[j] = on ? xload(jj, k0 + (c0 + 64 * u) * 8) : u32x4{0u, 0u, 0u, 0u};
 #endif
                 }
+#if HB_FORM == 2
+                // Inline asm: the builtin on words extracted from these
+                // vectors was miscompiled (every e got e=0's operands) by
+                // this image's compiler.  The asm keeps its order, so the
+                // word index e is outermost: consecutive dot2s update
+                // different sums (each sum still takes e = 0..3 in turn)
+                // instead of one dependent chain of four.
+                float t[RB][MV];  // the sums as locals (asm operands)
+#pragma unroll
+                for (u32 r = 0; r < RB; r++)
+#pragma unroll
+                    for (u32 j = 0; j < MV; j++) t[r][j] = acc[r][j];
+#pragma unroll
+                for (u32 e = 0; e < 4; e++)
+#pragma unroll
+                    for (u32 j = 0; j < MV; j++)
+#pragma unroll
+                        for (u32 r = 0; r < RB; r++)
+                            asm volatile("v_dot2c_f32_bf16 %0, %1, %2"
+                                         : "+v"(t[r][j])
+                                         : "v"(wv[u][r][e]), "v"(xs[j][e]));
+#pragma unroll
+                for (u32 r = 0; r < RB; r++)
+#pragma unroll
+                    for (u32 j = 0; j < MV; j++) acc[r][j] = t[r][j];
+#else
 #pragma unroll
                 for (u32 j = 0; j < MV; j++) {
                     const u32x4 xv = xs[j];
@@ -295,19 +339,13 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
                         float a = acc[r][j];
 #pragma unroll
                         for (u32 e = 0; e < 4; e++) {
-#if HB_FORM == 2
-                            // Inline asm: the builtin on words extracted from
-                            // these vectors was miscompiled (every e got e=0's
-                            // operands) by this image's compiler.
-                            asm volatile("v_dot2c_f32_bf16 %0, %1, %2" : "+v"(a) : "v"(wv[u][r][e]), "v"(xv[e]));
-#else
                             a = __builtin_fmaf(bf16_lo(wv[u][r][e]), bf16_lo(xv[e]), a);
                             a = __builtin_fmaf(bf16_hi(wv[u][r][e]), bf16_hi(xv[e]), a);
-#endif
                         }
                         acc[r][j] = a;
                     }
                 }
+#endif
             }
         };
         for (u32 bi = 0; bi < NFULL; bi++) block(bi * BLK + lane, HbTrue{});
@@ -347,6 +385,64 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
         for (u32 u = 0; u < NA; u++) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
         constexpr u32 BLOCK = 32 * U;  // K per unrolled block
         u32 kk = 0;
+#if HB_FORM == 3
+        // W through a wave-private LDS tile: a block's 16 rows x 32*U K are
+        // U load instructions of 16-byte chunks in row order (instruction
+        // i, lane l: row i*RPI + l/CPR, chunk l%CPR; 256 B, 512 B or 1 KB of
+        // one row per 16, 32 or 64 lanes), written to the tile with the chunk index
+        // XORed by the row, then read back as the A operand (lane (fr, fq):
+        // row fr, chunk 4u + fq; 16 lanes of one chunk column hit 16
+        // distinct 16-byte bank groups).  The next block's loads are issued
+        // before this block's LDS writes and MFMAs.
+        constexpr u32 CPR = 4 * U;  // chunks per row per block
+        u32x4* tile = wtile + wave * (16 * CPR);
+        constexpr u32 RPI = 64 / CPR;  // rows per load instruction
+        const u32 lr = lane / CPR, lc = lane % CPR;
+        // The last workgroup's waves past the last row block have n0 >= N:
+        // their base is row N-1 (their sums are never stored).
+        const u32 nb0 = n0 < N ? n0 : N - 1;
+        const u16* wrow0 = W + (u64)nb0 * K + k0 + lc * 8;
+        auto wload = [&](u32x4 (&v)[U], u32 at) HB_INLINE2 {
+#pragma unroll
+            for (u32 i = 0; i < U; i++) {
+                const u32 r = i * RPI + lr;
+                const u32 rr = nb0 + r < N ? r : N - 1 - nb0;  // rows past N read row N-1
+                v[i] = __builtin_nontemporal_load((const u32x4*)(wrow0 + at + rr * K));
+            }
+        };
+        auto wstep = [&](u32x4 (&v)[U], u32 at) HB_INLINE2 {
+#pragma unroll
+            for (u32 i = 0; i < U; i++) {
+                const u32 r = i * RPI + lr;
+                tile[r * CPR + (lc ^ (r & (CPR - 1)))] = v[i];
+            }
+            u32x4 xv[U];
+#pragma unroll
+            for (u32 u = 0; u < U; u++)
+                xv[u] = xon ? *(const u32x4*)(xrow + at + (u * 4 + fq) * 8) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+            for (u32 u = 0; u < U; u++) {
+                const u32x4 a = tile[fr * CPR + ((u * 4 + fq) ^ (fr & (CPR - 1)))];
+                acc[u % NA] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                                      __builtin_bit_cast(bf16x8, xv[u]),
+                                                                      acc[u % NA], 0, 0, 0);
+            }
+        };
+        constexpr u32 NB = KS / BLOCK;  // whole blocks
+        if constexpr (NB > 0) {
+            u32x4 va[U], vb[U];
+            wload(va, 0);
+            for (u32 b = 0; b < NB; b += 2) {
+                if (b + 1 < NB) wload(vb, (b + 1) * BLOCK);
+                wstep(va, b * BLOCK);
+                if (b + 1 < NB) {
+                    if (b + 2 < NB) wload(va, (b + 2) * BLOCK);
+                    wstep(vb, (b + 1) * BLOCK);
+                }
+            }
+            kk = NB * BLOCK;
+        }
+#else
         for (; kk + BLOCK <= KS; kk += BLOCK) {
             u32x4 wv[U], xv[U];
 #pragma unroll
@@ -361,6 +457,7 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
                                                                       __builtin_bit_cast(bf16x8, xv[u]),
                                                                       acc[u % NA], 0, 0, 0);
         }
+#endif
         for (; kk < KS; kk += 32) {
             const u32x4 wv = *(const u32x4*)(wrow + kk + fq * 8);
             const u32x4 xv = xon ? *(const u32x4*)(xrow + kk + fq * 8) : u32x4{0u, 0u, 0u, 0u};
@@ -374,7 +471,7 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
 #endif
 
         // ---- fold the SPLIT partials in wave order, then Out ----
-#if HB_FORM != 1
+#if !HB_MMA
         if constexpr (SPLIT > 1) {
             if (owner) part[(wave * RB + own_r) * 16 + own_j] = mine;
             __syncthreads();

@@ -127,7 +127,9 @@ typedef struct hb_desc {
     /* matvec: rows of x (1..16), waves sharing a row block's K (split),
      * persistent workgroups (0 = one per row block), W rows per wave
      * (VALU form), form (0 VALU lanes-stride-K, 1 MFMA, 2 the VALU layout with
-     * v_dot2_f32_bf16: two products added per instruction, no conversion). */
+     * v_dot2_f32_bf16: two products added per instruction, no conversion;
+     * 3 MFMA with W loaded in row order and turned into the A operand
+     * through a per-wave LDS tile, unroll 4, 8 or 16). */
     uint32_t mv_m, split, persist, rows, form;
     /* MoE: slots per row (top_k), experts, the tile table's capacity
      * (moe_tiles, prefill.rs:832-835), rows of the largest block. */

@@ -265,7 +265,7 @@ def test_descriptor_refusals(gpu):
     """Fields a kernel cannot honour are refused at build, naming the rule:
     w_nt without direct-to-LDS staging, x_lds past 64 KiB of x (144 KiB with
     8 or 16 waves; or on the MFMA matvec), matvec waves other than 4, 8, 16
-    (4 for XSrc::Norm), a combine of more than 16 slots."""
+    (4 for XSrc::Norm), form 3 with an unroll other than 4, 8, 16, a combine of more than 16 slots."""
     with pytest.raises(hb.HerbertError, match="w_nt"):
         gpu.pipeline(hb.gemm_mma(256, 512, 0, bm=128, bn=128, bk=64, wm=2, wn=2, mfma=16, dbuf=1,
                                  lds_dma=0, w_nt=1))
@@ -275,6 +275,8 @@ def test_descriptor_refusals(gpu):
         gpu.pipeline(hb.matvec(2560, 4608, 0, mv_m=4, form=1, x_lds=True))
     with pytest.raises(hb.HerbertError, match="x_lds"):  # 144 KiB + 16 bytes
         gpu.pipeline(hb.matvec(9216 + 8, 2560, 0, mv_m=8, rows=1, form=2, x_lds=True, waves=16))
+    with pytest.raises(hb.HerbertError, match="W through LDS"):
+        gpu.pipeline(hb.matvec(2560, 4608, 0, mv_m=4, form=3, unroll=6))
     with pytest.raises(hb.HerbertError, match="mv_waves"):
         gpu.pipeline(hb.matvec(2560, 4608, 0, mv_m=4, form=2, waves=12))
     with pytest.raises(hb.HerbertError, match="Norm"):
