@@ -58,7 +58,7 @@ hb_desc with_defaults(const hb_desc& in) {
         if (!d.split) d.split = 1;
         if (!d.rows) d.rows = 4;
         if (!d.unroll) d.unroll = 4;
-        if (d.form == 1 || d.form == 3) d.rows = 16;
+        if (d.form == 1 || (d.form == 3 && d.rows != 32)) d.rows = 16;
         if (!d.mv_waves) d.mv_waves = 4;
     }
     return d;
@@ -185,14 +185,17 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
                 return fail(HB_ERR_UNSUPPORTED,
                             "matvec x_lds: VALU forms, m*k*2 <= 64 KiB of LDS (144 KiB with 8 or 16 waves)");
             const bool xl = d.x_lds && d.xsrc != HB_XSRC_NORM;
-            if (!d.k || !d.n || d.k % (8 * d.split) || (d.split != 1 && d.split != 2 && d.split != 4))
-                return fail(HB_ERR_UNSUPPORTED, "matvec: K a multiple of 8*split, split 1, 2 or 4");
+            if (!d.k || !d.n || d.k % (8 * d.split) || !d.split || (d.split & (d.split - 1)) ||
+                d.split > d.mv_waves)
+                return fail(HB_ERR_UNSUPPORTED, "matvec: K a multiple of 8*split, split 1, 2, 4 (8, 16 with as many waves)");
             if (!mma && (d.rows > 8 || !d.rows || d.rows * d.mv_m > 64 || d.mv_m > 16))
                 return fail(HB_ERR_UNSUPPORTED, "matvec: rows 1..8, rows*m <= 64");
             if (mma && (d.mv_m > 16 || (d.k / d.split) % 32))
                 return fail(HB_ERR_UNSUPPORTED, "matvec (MFMA): m <= 16, K/split a multiple of 32");
-            if (d.form == 3 && ((d.unroll != 4 && d.unroll != 8 && d.unroll != 16) || d.mv_waves * d.unroll > 64))
-                return fail(HB_ERR_UNSUPPORTED, "matvec (MFMA, W through LDS): unroll 4, 8 or 16, waves*unroll <= 64");
+            if (d.form == 3 && ((d.unroll != 4 && d.unroll != 8 && d.unroll != 16) ||
+                                d.mv_waves * d.unroll * (d.rows / 16) > 64))
+                return fail(HB_ERR_UNSUPPORTED,
+                            "matvec (MFMA, W through LDS): unroll 4, 8 or 16, waves*unroll*rows/16 <= 64");
             if (!d.unroll || d.unroll > (mma ? 16u : 8u))
                 return fail(HB_ERR_UNSUPPORTED, "matvec: unroll 1..8 (MFMA form 1..16)");
             char xtag[48] = "";
@@ -340,7 +343,7 @@ uint32_t groups_of(const hb_desc& d, uint32_t m) {
             return cdiv(m, bm) * nt;                                 // gemm_mma_groups
         }
         case HB_KIND_MATVEC: {  // matvec_groups / matvec_split_groups / matvec_full_groups
-            uint32_t rb = d.form == 1 || d.form == 3 ? 16 : d.rows, per = d.mv_waves / d.split;
+            uint32_t rb = d.form == 1 ? 16 : d.rows, per = d.mv_waves / d.split;
             uint32_t n = d.n;
             if (d.out == HB_OUT_SWIGLU) n /= 2, rb /= 2;  // output rows: gate rows
             uint32_t wgs = cdiv(cdiv(n, rb), per);

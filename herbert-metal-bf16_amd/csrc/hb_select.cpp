@@ -884,12 +884,15 @@ int hb_engine_matvec_fused(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, u
     // LDS tile (form 3): for several rows, where the VALU forms run out of
     // issue (measured at m=8: gate_up 4.4 -> 5.0 TB/s, lm_head 5.3 -> 6.1).
     if (mv_m > 1 && !fused && k % 128 == 0) {
-        struct F { uint32_t unroll, split, persist; };
-        for (F f : {F{4, 4, 0}, F{4, 2, 0}, F{4, 1, 512}, F{4, 4, 512}, F{8, 2, 0}, F{8, 4, 0}, F{8, 4, 512}}) {
-            hb_desc d3 = desc(3, 16, f.split, f.persist);
+        // rows 32: two 16-row tiles per wave share each x fragment (half
+        // the x loads per W byte; lm_head at m=8: 6.1 -> 6.7 TB/s).
+        struct F { uint32_t unroll, split, persist, rows; };
+        for (F f : {F{4, 4, 0, 16}, F{4, 2, 0, 16}, F{4, 1, 512, 16}, F{4, 4, 512, 16}, F{8, 2, 0, 16},
+                    F{8, 4, 0, 16}, F{8, 4, 512, 16}, F{4, 4, 0, 32}, F{4, 4, 512, 32}}) {
+            hb_desc d3 = desc(3, f.rows, f.split, f.persist);
             d3.unroll = f.unroll;
-            add("mfl_u" + std::to_string(f.unroll) + "k" + std::to_string(f.split) +
-                    (f.persist ? "p" + std::to_string(f.persist) : ""), d3);
+            add("mfl" + std::string(f.rows == 32 ? "_r32" : "") + "_u" + std::to_string(f.unroll) + "k" +
+                    std::to_string(f.split) + (f.persist ? "p" + std::to_string(f.persist) : ""), d3);
         }
     }
     for (uint32_t split : splits)

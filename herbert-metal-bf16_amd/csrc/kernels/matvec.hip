@@ -63,6 +63,8 @@ static_assert(WAVES == 4 || WAVES == 8 || WAVES == 16, "4, 8 or 16 waves");
 constexpr u32 GROUPS_PER_WG = WAVES / SPLIT;  // row blocks per workgroup
 #if !HB_MMA
 constexpr u32 RB = HB_ROWS;                   // rows per row block
+#elif HB_FORM == 3
+constexpr u32 RB = HB_ROWS == 32 ? 32 : 16;   // one or two 16-row MFMA tiles
 #else
 constexpr u32 RB = 16;
 #endif
@@ -90,6 +92,7 @@ constexpr u32 RB = 16;
 // Out::Swiglu (HB_OUT 3): W's rows are [gate (N/2) | up (N/2)]; a row
 // block's RB rows are RB/2 gate rows and the same rows' up rows, and it
 // writes RB/2 outputs.
+constexpr u32 T = RB / 16;  // MFMA forms: 16-row tiles per wave (2 only in form 3)
 constexpr bool SWO = OUT == 3;
 constexpr u32 NOUT = SWO ? N / 2 : N;         // output rows
 constexpr u32 RO = SWO ? RB / 2 : RB;         // output rows per row block
@@ -140,8 +143,8 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
                                                            u32 m_launch) {
     __shared__ float part[SPLIT > 1 ? WAVES * RB * 16 : 1];
 #if HB_FORM == 3
-    static_assert((U == 4 || U == 8 || U == 16) && WAVES * U <= 64, "W through LDS: unroll 4, 8 or 16, WAVES*U KiB of tile");
-    __shared__ u32x4 wtile[WAVES * 16 * 4 * U];
+    static_assert((U == 4 || U == 8 || U == 16) && WAVES * U * T <= 64, "W through LDS: unroll 4, 8 or 16, WAVES*U*T KiB of tile");
+    __shared__ u32x4 wtile[WAVES * RB * 4 * U];
 #endif
     const u32 tid = threadIdx.x, lane = tid & 63u;
     const u32 wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -373,64 +376,78 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
                     if (lane == r * MV + j) mine_u = acc[r + RO][j];
         }
 #else
-        // ---- MFMA: 16 rows x (m <= 16) columns per wave ----
+        // ---- MFMA: T tiles of 16 rows x (m <= 16) columns per wave ----
         const u32 fr = lane & 15u, fq = lane >> 4;
-        u32 n = n0 + fr;
-        const u16* wrow = W + (u64)(n < N ? n : N - 1) * K + k0;
         const bool xon = fr < m;
         const u16* xrow = x + (u64)(xon ? fr : 0) * K + k0;
-        constexpr u32 NA = U < 4 ? U : 4;  // independent accumulators
-        f32x4 acc[NA];
+        const u16* wrow[T];  // the A operand's row (fr) of each tile
 #pragma unroll
-        for (u32 u = 0; u < NA; u++) acc[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (u32 t = 0; t < T; t++) {
+            const u32 n = n0 + 16 * t + fr;
+            wrow[t] = W + (u64)(n < N ? n : N - 1) * K + k0;
+        }
+        constexpr u32 NA = U < 4 ? U : 4;  // independent accumulators per tile
+        f32x4 acc[T][NA];
+#pragma unroll
+        for (u32 t = 0; t < T; t++)
+#pragma unroll
+            for (u32 u = 0; u < NA; u++) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
         constexpr u32 BLOCK = 32 * U;  // K per unrolled block
         u32 kk = 0;
 #if HB_FORM == 3
-        // W through a wave-private LDS tile: a block's 16 rows x 32*U K are
-        // U load instructions of 16-byte chunks in row order (instruction
-        // i, lane l: row i*RPI + l/CPR, chunk l%CPR; 256 B, 512 B or 1 KB of
-        // one row per 16, 32 or 64 lanes), written to the tile with the chunk index
-        // XORed by the row, then read back as the A operand (lane (fr, fq):
-        // row fr, chunk 4u + fq; 16 lanes of one chunk column hit 16
-        // distinct 16-byte bank groups).  The next block's loads are issued
+        // W through a wave-private LDS tile: a block's 16*T rows x 32*U K
+        // are T*U load instructions of 16-byte chunks in row order
+        // (instruction i, lane l: row i*RPI + l/CPR, chunk l%CPR; 256 B,
+        // 512 B or 1 KB of one row per 16, 32 or 64 lanes), written to the
+        // tile with the chunk index XORed by the row, then read back as the
+        // A operands (lane (fr, fq): row 16t + fr, chunk 4u + fq; 16 lanes
+        // of one chunk column hit 16 distinct 16-byte bank groups).  Each x
+        // fragment serves the T tiles.  The next block's loads are issued
         // before this block's LDS writes and MFMAs.
         constexpr u32 CPR = 4 * U;  // chunks per row per block
-        u32x4* tile = wtile + wave * (16 * CPR);
+        constexpr u32 LI = T * U;   // load instructions per block
+        u32x4* tile = wtile + wave * (16 * T * CPR);
         constexpr u32 RPI = 64 / CPR;  // rows per load instruction
         const u32 lr = lane / CPR, lc = lane % CPR;
         // The last workgroup's waves past the last row block have n0 >= N:
         // their base is row N-1 (their sums are never stored).
         const u32 nb0 = n0 < N ? n0 : N - 1;
         const u16* wrow0 = W + (u64)nb0 * K + k0 + lc * 8;
-        auto wload = [&](u32x4 (&v)[U], u32 at) HB_INLINE2 {
+        auto wload = [&](u32x4 (&v)[LI], u32 at) HB_INLINE2 {
 #pragma unroll
-            for (u32 i = 0; i < U; i++) {
+            for (u32 i = 0; i < LI; i++) {
                 const u32 r = i * RPI + lr;
                 const u32 rr = nb0 + r < N ? r : N - 1 - nb0;  // rows past N read row N-1
                 v[i] = __builtin_nontemporal_load((const u32x4*)(wrow0 + at + rr * K));
             }
         };
-        auto wstep = [&](u32x4 (&v)[U], u32 at) HB_INLINE2 {
+        auto wstep = [&](u32x4 (&v)[LI], u32 at) HB_INLINE2 {
 #pragma unroll
-            for (u32 i = 0; i < U; i++) {
+            for (u32 i = 0; i < LI; i++) {
                 const u32 r = i * RPI + lr;
                 tile[r * CPR + (lc ^ (r & (CPR - 1)))] = v[i];
             }
             u32x4 xv[U];
 #pragma unroll
             for (u32 u = 0; u < U; u++)
+#if HB_PROBE_NOX  // development probe: no x loads (wrong results)
+                xv[u] = u32x4{fr, u, fq, at};
+#else
                 xv[u] = xon ? *(const u32x4*)(xrow + at + (u * 4 + fq) * 8) : u32x4{0u, 0u, 0u, 0u};
+#endif
 #pragma unroll
-            for (u32 u = 0; u < U; u++) {
-                const u32x4 a = tile[fr * CPR + ((u * 4 + fq) ^ (fr & (CPR - 1)))];
-                acc[u % NA] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
-                                                                      __builtin_bit_cast(bf16x8, xv[u]),
-                                                                      acc[u % NA], 0, 0, 0);
-            }
+            for (u32 u = 0; u < U; u++)
+#pragma unroll
+                for (u32 t = 0; t < T; t++) {
+                    const u32 r = 16 * t + fr;
+                    const u32x4 a = tile[r * CPR + ((u * 4 + fq) ^ (r & (CPR - 1)))];
+                    acc[t][u % NA] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                        __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, xv[u]), acc[t][u % NA], 0, 0, 0);
+                }
         };
         constexpr u32 NB = KS / BLOCK;  // whole blocks
         if constexpr (NB > 0) {
-            u32x4 va[U], vb[U];
+            u32x4 va[LI], vb[LI];
             wload(va, 0);
             for (u32 b = 0; b < NB; b += 2) {
                 if (b + 1 < NB) wload(vb, (b + 1) * BLOCK);
@@ -447,27 +464,32 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
             u32x4 wv[U], xv[U];
 #pragma unroll
             for (u32 u = 0; u < U; u++)
-                wv[u] = __builtin_nontemporal_load((const u32x4*)(wrow + kk + (u * 4 + fq) * 8));
+                wv[u] = __builtin_nontemporal_load((const u32x4*)(wrow[0] + kk + (u * 4 + fq) * 8));
 #pragma unroll
             for (u32 u = 0; u < U; u++)
                 xv[u] = xon ? *(const u32x4*)(xrow + kk + (u * 4 + fq) * 8) : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
             for (u32 u = 0; u < U; u++)
-                acc[u % NA] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wv[u]),
-                                                                      __builtin_bit_cast(bf16x8, xv[u]),
-                                                                      acc[u % NA], 0, 0, 0);
+                acc[0][u % NA] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wv[u]),
+                                                                         __builtin_bit_cast(bf16x8, xv[u]),
+                                                                         acc[0][u % NA], 0, 0, 0);
         }
 #endif
         for (; kk < KS; kk += 32) {
-            const u32x4 wv = *(const u32x4*)(wrow + kk + fq * 8);
             const u32x4 xv = xon ? *(const u32x4*)(xrow + kk + fq * 8) : u32x4{0u, 0u, 0u, 0u};
-            acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wv),
-                                                             __builtin_bit_cast(bf16x8, xv), acc[0],
-                                                             0, 0, 0);
+#pragma unroll
+            for (u32 t = 0; t < T; t++) {
+                const u32x4 wv = *(const u32x4*)(wrow[t] + kk + fq * 8);
+                acc[t][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wv),
+                                                                    __builtin_bit_cast(bf16x8, xv), acc[t][0],
+                                                                    0, 0, 0);
+            }
         }
 #pragma unroll
-        for (u32 u = 1; u < NA; u++) acc[0] += acc[u];
-        // Lane (fr, fq) holds rows 4*fq..+3 of the block for x row fr.
+        for (u32 t = 0; t < T; t++)
+#pragma unroll
+            for (u32 u = 1; u < NA; u++) acc[t][0] += acc[t][u];
+        // Lane (fr, fq) holds rows 16t + 4*fq..+3 of the block for x row fr.
 #endif
 
         // ---- fold the SPLIT partials in wave order, then Out ----
@@ -498,24 +520,31 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
 #else
         if constexpr (SPLIT > 1) {
 #pragma unroll
-            for (u32 i = 0; i < 4; i++) part[(wave * 16 + 4 * fq + i) * 16 + fr] = acc[0][i];
+            for (u32 t = 0; t < T; t++)
+#pragma unroll
+                for (u32 i = 0; i < 4; i++) part[(wave * RB + 16 * t + 4 * fq + i) * 16 + fr] = acc[t][0][i];
             __syncthreads();
             if (sp == 0) {
 #pragma unroll
-                for (u32 i = 0; i < 4; i++) {
-                    float s = 0.0f;
+                for (u32 t = 0; t < T; t++)
 #pragma unroll
-                    for (u32 q = 0; q < SPLIT; q++) s += part[((gi * SPLIT + q) * 16 + 4 * fq + i) * 16 + fr];
-                    acc[0][i] = s;
-                }
+                    for (u32 i = 0; i < 4; i++) {
+                        float s = 0.0f;
+#pragma unroll
+                        for (u32 q = 0; q < SPLIT; q++)
+                            s += part[((gi * SPLIT + q) * RB + 16 * t + 4 * fq + i) * 16 + fr];
+                        acc[t][0][i] = s;
+                    }
             }
         }
         if (sp == 0 && fr < m) {
 #pragma unroll
-            for (u32 i = 0; i < 4; i++) {
-                const u32 nn = n0 + 4 * fq + i;
-                if (nn < N) store_out(y, (u64)fr * N + nn, acc[0][i]);
-            }
+            for (u32 t = 0; t < T; t++)
+#pragma unroll
+                for (u32 i = 0; i < 4; i++) {
+                    const u32 nn = n0 + 16 * t + 4 * fq + i;
+                    if (nn < N) store_out(y, (u64)fr * N + nn, acc[t][0][i]);
+                }
         }
 #endif
         if constexpr (SPLIT > 1) __syncthreads();  // part[] reused by the next block

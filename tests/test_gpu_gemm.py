@@ -277,6 +277,8 @@ def test_descriptor_refusals(gpu):
         gpu.pipeline(hb.matvec(9216 + 8, 2560, 0, mv_m=8, rows=1, form=2, x_lds=True, waves=16))
     with pytest.raises(hb.HerbertError, match="W through LDS"):
         gpu.pipeline(hb.matvec(2560, 4608, 0, mv_m=4, form=3, unroll=6))
+    with pytest.raises(hb.HerbertError, match="W through LDS"):  # 4 waves x 16 x 2 tiles: 128 KiB
+        gpu.pipeline(hb.matvec(2560, 4608, 0, mv_m=4, form=3, unroll=16, rows=32))
     with pytest.raises(hb.HerbertError, match="mv_waves"):
         gpu.pipeline(hb.matvec(2560, 4608, 0, mv_m=4, form=2, waves=12))
     with pytest.raises(hb.HerbertError, match="Norm"):

@@ -26,6 +26,7 @@ FORMS = {
     "mfl_u4_k4": dict(form=3, split=4, unroll=4),
     "mfl_u8_k2_p": dict(form=3, split=2, persist=512, unroll=8),
     "mfl_u16": dict(form=3, split=1, unroll=16),
+    "mfl_r32_u4_k4": dict(form=3, rows=32, split=4, unroll=4),
 }
 
 
@@ -74,25 +75,29 @@ def test_matvec_lm_head(gpu, form, m):
     check_close(got, want, k, abs_products(x, w), "lm_head %s m=%d" % (form, m))
 
 
+@pytest.mark.parametrize("rows", [16, 32])
 @pytest.mark.parametrize("u,split,persist", [(4, 1, 0), (8, 1, 0), (16, 2, 0), (8, 4, 7), (4, 2, 3)])
 @pytest.mark.parametrize("k,n", [(1056, 100), (4096, 33), (2560, 4608)])
-def test_matvec_w_through_lds_equals_mfma(gpu, k, n, u, split, persist):
+def test_matvec_w_through_lds_equals_mfma(gpu, k, n, u, split, persist, rows):
     """Form 3 (W read in row order, turned into the MFMA A operand through a
     per-wave LDS tile) runs form 1's MFMAs on the same operands: bit-equal
     to form 1, with N not a multiple of the 16-row block (rows past N read
     row N-1, never stored), K / split not a multiple of the 32*unroll block
     (the tail in form 1's loads), and a few persistent workgroups looping
-    over the row blocks; within the contract of the oracle."""
+    over the row blocks; rows 32: two 16-row tiles per wave, each the same
+    MFMAs as form 1's tile; within the contract of the oracle."""
     if (k // split) % 32:
         pytest.skip("K/split a multiple of 32")
+    if rows == 32 and 4 * u * 2 > 64:
+        pytest.skip("4 waves x unroll x 2 tiles: more than 64 KiB of LDS")
     m = 5
     x = hb.normal_bf16(0x5EED0041, 1.0, (m, k))
     w = hb.normal_bf16(0x5EED0042, 0.02, (n, k))
     y0 = hb.normal_bf16(27, 1.0, (m, n))
     f = dict(split=split, persist=persist, unroll=u)
-    got = run_mv(gpu, x, w, 2, y0, form=3, **f)
+    got = run_mv(gpu, x, w, 2, y0, form=3, rows=rows, **f)
     ref = run_mv(gpu, x, w, 2, y0, form=1, **f)
-    assert np.array_equal(got, ref), "form 3 differs from form 1 (k=%d n=%d %s)" % (k, n, f)
+    assert np.array_equal(got, ref), "form 3 differs from form 1 (k=%d n=%d rows=%d %s)" % (k, n, rows, f)
     check_close(got, orc.gemm(x, w, orc.OUT_RESIDUAL, y0), k, abs_products(x, w), "form 3 %d x %d" % (k, n),
                 acc=orc.gemm(x, w, orc.OUT_F32))
 
