@@ -309,6 +309,13 @@ def trace_summary(trace_csv, bench_json, cmd):
         for g, nm in mv["kernels"].items():
             n, a = avg_of(nm)
             out.append("  %-8s %-52s calls %5d  avg %7.2f us" % (g, nm, n, a))
+        for mk in ("m4", "m8"):
+            if mk in mv:
+                out += ["decode (M=%s) kernels, the same averages; step %.1f GB/s (%.1f%% of HBM):" % (
+                    mk[1:], mv[mk]["value"], 100 * mv[mk]["frac"])]
+                for g, nm in mv[mk]["kernels"].items():
+                    n, a = avg_of(nm)
+                    out.append("  %-8s %-52s calls %5d  avg %7.2f us" % (g, nm, n, a))
     moe = b.get("moe")
     if moe:
         out += ["", "MoE layer (config 5): bench per-op times, and the grouped GEMMs' rocprof averages:"]
