@@ -92,6 +92,36 @@ def test_matvec_autotune_cold(gpu):
         gpu.free(b)
 
 
+@pytest.mark.parametrize("k,n,out", [(2560, 4608, 0), (9216, 2560, 2)])
+def test_matvec_autotune_eight_rows(gpu, k, n, out):
+    """At 8 rows the candidates include form 3 (MFMA, W through LDS; 16 and
+    32 rows per wave) and the 16-wave workgroups staging x once per CU (down:
+    144 KiB of x): they build, are timed under their names, and the pick
+    computes the contract."""
+    m = 8
+    w = hb.normal_bf16(41, 0.02, (n, k))
+    x = hb.normal_bf16(42, 1.0, (m, k))
+    y0 = hb.normal_bf16(43, 1.0, (m, n)) if out == 2 else None
+    Wb, X = gpu.alloc_with(w), gpu.alloc_with(x)
+    Y = gpu.alloc_with(y0) if y0 is not None else gpu.alloc(m * n * 2)
+    try:
+        with hb.Engine(gpu, "") as e:
+            kern = e.mv(k, n, out, m, [hb.r(Wb)], hb.r(X), hb.r(Y))
+            log = e.log()
+        assert "not built" not in log, log
+        assert re.search(r"mfl_u4k4", log) and re.search(r"mfl_r32_u4k4", log), log
+        assert re.search(r"xl_w16", log), log
+        if y0 is not None:
+            gpu.upload(Y, y0)
+        gpu.launch(kern, [hb.r(Wb), hb.r(X), hb.r(Y)], m)
+        got = gpu.download(Y, np.uint16, m * n).reshape(m, n)
+        acc = orc.gemm(x, w, orc.OUT_F32) if out == 2 else None
+        check_close(got, orc.gemm(x, w, out, y0), k, abs_products(x, w), "mv pick m=8 %dx%d" % (k, n), acc=acc)
+    finally:
+        for b in (Wb, X, Y):
+            gpu.free(b)
+
+
 def test_matvec_fused_autotune(gpu):
     """mv_full with its fusions (qwen.rs:1311-1336): the pick of a decode
     layer's gate|up with XSrc::Norm and Out::Swiglu, then the down with
