@@ -124,14 +124,14 @@ typedef struct hb_desc {
      * LDS swizzle (0 = conflict-free for the K step, s + 1 = shift s), tile
      * order (0 plain, 1 XCD-contiguous). 0 = the kind's default. */
     uint32_t bm, bn, bk, wm, wn, mfma, dbuf, swz, order;
-    /* matvec: rows of x (1..16), waves sharing a row block's K (split: 1,
-     * 2, 4; 8 and 16 with at least as many mv_waves),
-     * persistent workgroups (0 = one per row block), W rows per wave
-     * (VALU forms; form 3: 16 or 32), form (0 VALU lanes-stride-K, 1 MFMA, 2 the VALU layout with
-     * v_dot2_f32_bf16: two products added per instruction, no conversion;
+    /* matvec: rows of x (1..16); waves sharing a row block's K (split: 1,
+     * 2, 4; 8 and 16 with at least as many mv_waves); persistent workgroups
+     * (0 = one per row block); W rows per wave (VALU forms 1..8; form 3: 16
+     * or 32); form: 0 VALU lanes-stride-K, 1 MFMA, 2 the VALU layout with
+     * v_dot2_f32_bf16 (two products added per instruction, no conversion),
      * 3 MFMA with W loaded in row order and turned into the A operand
-     * through a per-wave LDS tile, unroll 4, 8 or 16, rows 16 or 32: one or
-     * two 16-row MFMA tiles sharing each x fragment). */
+     * through a per-wave LDS tile (unroll 4, 8 or 16; rows 32: two 16-row
+     * MFMA tiles sharing each x fragment). */
     uint32_t mv_m, split, persist, rows, form;
     /* MoE: slots per row (top_k), experts, the tile table's capacity
      * (moe_tiles, prefill.rs:832-835), rows of the largest block. */
@@ -151,7 +151,8 @@ typedef struct hb_desc {
      * plus_one (weights used as w + 1). */
     uint32_t xsrc, eps_bits, plus_one;
     /* matvec (VALU forms): 1 = the x rows (plain, or XSrc::Swiglu's h) are
-     * staged once per workgroup into LDS (m*k*2 <= 64 KiB) and every row
+     * staged once per workgroup into LDS (m*k*2 <= 64 KiB; 144 KiB with
+     * 8 or 16 mv_waves) and every row
      * block reads them from there; XSrc::Norm always does. */
     uint32_t x_lds;
     /* MFMA GEMM, direct-to-LDS: 1 = W's loads marked non-temporal (nt), for
