@@ -134,6 +134,27 @@ HB_DEV float wave_sum(float v) {
     return v;
 }
 
+// The 64 lanes' sum of the matvec's row sums without the LDS crossbar:
+// pairs (quad_perm 1,0,3,2), quads (2,3,0,1), then the half-row and row
+// mirrors (once each 4- and 8-lane group is uniform, the mirrored lane
+// holds the other group's value), the 16-lane halves of each 32 by a
+// swizzle (xor 16), and the two 32-lane halves read as scalars.  Every
+// lane ends with the same value; the association is this tree's.
+template <int CTRL>
+HB_DEV float dpp_add(float v) {
+    return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                      0xf, 0xf, true));
+}
+HB_DEV float wave_sum_rows(float v) {
+    v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
+    v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
+    v = dpp_add<0x141>(v);  // row_half_mirror
+    v = dpp_add<0x140>(v);  // row_mirror
+    v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 0)) +
+           __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 32));
+}
+
 extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__ W,
                                                            const u16* __restrict__ x,
                                                            void* __restrict__ y,
@@ -353,10 +374,21 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
         };
         for (u32 bi = 0; bi < NFULL; bi++) block(bi * BLK + lane, HbTrue{});
         if constexpr (REM != 0) block(NFULL * BLK + lane, HbFalse{});
+#if HB_FORM == 2
+        // The sums' last writers are asm statements, which the compiler's
+        // wait-state padding before a DPP read of their results may not
+        // count: two wait states here, and every sum passed through an asm
+        // after them, so no DPP read is scheduled above the s_nop.
+        asm volatile("s_nop 1");
 #pragma unroll
         for (u32 r = 0; r < RB; r++)
 #pragma unroll
-            for (u32 j = 0; j < MV; j++) acc[r][j] = wave_sum(acc[r][j]);
+            for (u32 j = 0; j < MV; j++) asm volatile("" : "+v"(acc[r][j]));
+#endif
+#pragma unroll
+        for (u32 r = 0; r < RB; r++)
+#pragma unroll
+            for (u32 j = 0; j < MV; j++) acc[r][j] = wave_sum_rows(acc[r][j]);
         // Lane r*MV + j owns (row r, x row j).
         float mine = 0.0f;
 #pragma unroll
