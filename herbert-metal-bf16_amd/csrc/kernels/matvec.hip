@@ -13,7 +13,7 @@
 //  0 (VALU, the reference's arithmetic layout): a wavefront computes ROWS
 //    consecutive rows of W over its K range; lane l takes the 16-byte
 //    chunks l, l+64, ... of it, UNROLL chunks per row in flight; then a
-//    butterfly sum over the 64 lanes.
+//    sum over the 64 lanes (DPP lane moves, wave_sum_rows).
 //  2 (dot2): form 0's layout, each pair of products added by one
 //    v_dot2_f32_bf16 (bf16 operands straight from the loaded words, f32
 //    sum): half the VALU instructions of form 0 and no conversions -- the
