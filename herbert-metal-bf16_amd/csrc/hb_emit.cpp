@@ -120,14 +120,25 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
                 return fail(HB_ERR_UNSUPPORTED, "gemm: stages 1..4 (1..2 through registers)");
             if (d.w_nt > 1 || (d.w_nt && !d.lds_dma))
                 return fail(HB_ERR_UNSUPPORTED, "gemm: w_nt with direct-to-LDS staging");
+            if (d.sched > 2) return fail(HB_ERR_INVALID, "gemm: sched 0, 1 or 2");
+            if (d.sched && (swi || experts || !d.lds_dma || d.wm * d.wn != 8 || d.dbuf < 2 ||
+                            d.w_nt || ((d.bm * d.bk / 8) % 64) || ((d.bn * d.bk / 8) % 64) ||
+                            d.bm * d.bk / 8 / 64 / 8 + d.bn * d.bk / 8 / 64 / 8 == 0))
+                return fail(HB_ERR_UNSUPPORTED,
+                            "gemm (ping-pong schedule): dense rows, direct-to-LDS, 8 waves, 3 or 4 "
+                            "stages, whole 1 KiB loads per stage, no w_nt");
+            if (d.sched &&
+                (uint64_t)(d.dbuf + 1) * (d.bm + d.bn) * d.bk * 2 > 160 * 1024)
+                return fail(HB_ERR_UNSUPPORTED, "gemm (ping-pong schedule): stages beyond 160 KiB of LDS");
             std::string band = d.band ? "_b" + std::to_string(d.band) : "";
             if (d.w_nt) band += "_wnt";
+            if (d.sched) band += d.sched == 1 ? "_pp" : "_pp2";
             snprintf(name, sizeof name, "gemm_mma%s_%ux%u_%s%s_t%ux%u_k%u_w%ux%u_x%u_d%u%s_s%u_o%u%s%s",
                      swi ? "_swiglu" : "", d.k, d.n, out_tag(d.out), d.m_first ? "_mf" : "", d.bn,
                      d.bm, d.bk, d.wn, d.wm, d.mfma, d.dbuf, d.lds_dma ? "_dma" : "", shift, d.order,
                      band.c_str(), rows.c_str());
             e->name = name;
-            e->source = "gemm_mfma.hip";
+            e->source = d.sched ? "gemm_pp.hip" : "gemm_mfma.hip";
             e->threads = 64 * d.wm * d.wn;
             e->nbind = 6;
             e->defines = {D("HB_K", d.k),        D("HB_N", d.n),       D("HB_OUT", d.out),
@@ -138,6 +149,7 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
                           D("HB_ORDER", d.order), D("HB_MFIRST", d.m_first ? 1 : 0),
                           D("HB_DMA", d.lds_dma ? 1 : 0), D("HB_SWIGLU", swi ? 1 : 0),
                           D("HB_BAND", d.band), D("HB_W_NT", d.w_nt)};
+            if (d.sched) e->defines.push_back(D("HB_GRP", d.sched - 1));
             return HB_OK;
         }
         case HB_KIND_GEMM_SIMT:
@@ -307,11 +319,14 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
     }
 }
 
-// Kernel development: HB_DEV_DEFINES="-DX=1 -DY=2" adds defines to every
-// kernel built while it is set (a variant under study); the kernel's name
-// (its cache key) then carries them.  Unset in production.
+// A development build of the library (build.py --dev, never the shipped
+// one) adds HB_DEV_DEFINES="-DX=1 -DY=2" to every kernel built while it is
+// set, for variants under study; the kernel's name (its cache key) then
+// carries them.  The shipped library has no such hook: no environment
+// variable changes what its kernels compute.
 int emit(const hb_desc& d, Emitted* e) {
     int rc = emit_kind(d, e);
+#ifdef HB_DEV_BUILD
     const char* dev = getenv("HB_DEV_DEFINES");
     if (rc || !dev || !*dev) return rc;
     std::string tag = "_dev";
@@ -327,7 +342,8 @@ int emit(const hb_desc& d, Emitted* e) {
         tag += isalnum((unsigned char)*c) ? *c : '_';
     }
     e->name += tag;
-    return HB_OK;
+#endif
+    return rc;
 }
 
 uint32_t groups_of(const hb_desc& d, uint32_t m) {

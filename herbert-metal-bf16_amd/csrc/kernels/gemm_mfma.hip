@@ -98,14 +98,6 @@ typedef __attribute__((ext_vector_type(FM == 16 ? 4 : 16))) float acc_t;
 
 HB_DEV u32 lpos(u32 r, u32 c) { return r * CH + (c ^ ((r >> HB_SWZ) & (CH - 1))); }
 
-// HB_PROBE_SKIP (kernel development only; wrong results): bit 0 drops the
-// global loads, bit 1 the MFMAs (their operands kept live), bit 2 the LDS
-// fragment reads (the registers kept, opaque), bit 3 sends every global load
-// past the buffer's range (the load instructions kept, no memory access) --
-// to time each part alone.
-#ifndef HB_PROBE_SKIP
-#define HB_PROBE_SKIP 0
-#endif
 // HB_W_NT 1: W's direct-to-LDS loads non-temporal (W read by one tile).
 #if defined(HB_W_NT) && HB_W_NT
 #define HB_W_CPOL " nt"
@@ -114,10 +106,7 @@ HB_DEV u32 lpos(u32 r, u32 c) { return r * CH + (c ^ ((r >> HB_SWZ) & (CH - 1)))
 #endif
 
 HB_DEV acc_t mfma(bf16x8 a, bf16x8 b, acc_t c) {
-#if HB_PROBE_SKIP & 2
-    asm volatile("" : "+v"(c) : "v"(a), "v"(b));
-    return c;
-#elif HB_MFMA == 16
+#if HB_MFMA == 16
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 #else
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
@@ -274,14 +263,12 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
         // offset past the buffer resource's range (0x7fffffff bytes), so
         // the load writes zeros to LDS without a memory access.
         if (HB_DMA && r >= rows) xoff[q] = 0x40000000u;
-        if (HB_PROBE_SKIP & 8) xoff[q] = 0x40000000u;
     }
 #pragma unroll
     for (u32 q = 0; q < W_LD; q++) {
         const u32 p = tid + q * NT, r = p / CH;
         const u32 cc = HB_DMA ? ((p % CH) ^ ((r >> HB_SWZ) & (CH - 1))) : p % CH;
         woff[q] = w_row(r) * K + cc * 8;
-        if (HB_PROBE_SKIP & 8) woff[q] = 0x40000000u;
     }
 
     acc_t acc[IN][IM];
@@ -303,11 +290,7 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     const u32 wbase = (wn * TN + fr) * CH, xbase = (wm * TM + fr) * CH;
     bf16x8 a[2][IN], b[2][IM];
     auto frag = [&](bf16x8& dst, const u32x4* p) HB_INLINE {
-#if HB_PROBE_SKIP & 4
-        asm volatile("" : "+v"(dst));
-#else
         dst = __builtin_bit_cast(bf16x8, *p);
-#endif
     };
     // Step s's fragments of a stage into a[h], b[h]: IN of W (A operand), IM
     // of X (B operand).
@@ -365,7 +348,6 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     // Load q of K tile kt's stage: q < X_LD an X chunk, else a W chunk.
     auto load_one = [&](u32 kt, u32x4* sX, u32x4* sW, u32 q) HB_INLINE {
         const u32 kb = kt * BK * 2;
-        if (HB_PROBE_SKIP & 1) return;
         if (q < X_LD)
             asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                          :: "s"(lds_addr(&sX[q * NT + wave * 64])), "v"(xoff[q] * 2), "s"(rX),
@@ -382,11 +364,6 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     };
     auto stx = [&](u32 i) HB_INLINE -> u32x4* { return sXa + i * XCHP; };
     auto stw = [&](u32 i) HB_INLINE -> u32x4* { return sWa + i * WCHP; };
-#if HB_PROBE_SKIP & 1
-    for (u32 i = tid; i < NS * XCHP; i += NT) sXa[i] = u32x4{i, 0, 0, 0};
-    for (u32 i = tid; i < NS * WCHP; i += NT) sWa[i] = u32x4{i, 0, 0, 0};
-    __syncthreads();
-#endif
     // Prologue: tiles 0..NS-2 in flight, tile 0 landed and published.
 #pragma unroll
     for (u32 t = 0; t + 1 < NS; t++)
@@ -456,13 +433,6 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
 #else
     u32x4 rx[X_LD], rw[W_LD];
     auto load = [&](u32 kt) HB_INLINE {
-#if HB_PROBE_SKIP & 1
-#pragma unroll
-        for (u32 q = 0; q < X_LD; q++) asm volatile("" : "+v"(rx[q]));
-#pragma unroll
-        for (u32 q = 0; q < W_LD; q++) asm volatile("" : "+v"(rw[q]));
-        return;
-#endif
 #pragma unroll
         for (u32 q = 0; q < X_LD; q++)
             if (XCH % NT == 0 || tid + q * NT < XCH) rx[q] = *(const u32x4*)(X + xoff[q] + kt * BK);

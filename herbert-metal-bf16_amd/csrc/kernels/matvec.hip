@@ -71,12 +71,6 @@ constexpr u32 RB = 16;
 #ifndef HB_XSRC
 #define HB_XSRC 0
 #endif
-#ifndef HB_PROBE_NOW
-#define HB_PROBE_NOW 0
-#endif
-#ifndef HB_PROBE_NOX
-#define HB_PROBE_NOX 0
-#endif
 #ifndef HB_XLDS
 #define HB_XLDS 0
 #endif
@@ -297,12 +291,8 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
                 const bool on = decltype(full)::value || (u * 64 + 64 <= REM) || (c0 + 64 * u < CHUNKS);
 #pragma unroll
                 for (u32 r = 0; r < RB; r++)
-#if HB_PROBE_NOW  // development probe: no W loads (wrong results)
-                    wv[u][r] = u32x4{lane + c0, u + r, lane ^ c0, (u32)(u64)wr[r]};
-#else
                     wv[u][r] = on ? __builtin_nontemporal_load((const u32x4*)(wr[r] + k0 + (c0 + 64 * u) * 8))
                                   : u32x4{0u, 0u, 0u, 0u};
-#endif
             }
 #if HB_XIN_LDS
             if (HOIST && pending) {
@@ -321,13 +311,7 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
 #pragma unroll
                 for (u32 j = 0; j < MV; j++) {
                     const u32 jj = j < m ? j : m - 1;
-#if HB_PROBE_NOX
-                    // Kernel development only (wrong results): no x loads, W stands in.
-                    xs[j] = wv[u][j % RB];
-                    (void)jj;
-#else
                     xs[j] = on ? xload(jj, k0 + (c0 + 64 * u) * 8) : u32x4{0u, 0u, 0u, 0u};
-#endif
                 }
 #if HB_FORM == 2
                 // Inline asm: the builtin on words extracted from these
@@ -462,11 +446,7 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
             u32x4 xv[U];
 #pragma unroll
             for (u32 u = 0; u < U; u++)
-#if HB_PROBE_NOX  // development probe: no x loads (wrong results)
-                xv[u] = u32x4{fr, u, fq, at};
-#else
                 xv[u] = xon ? *(const u32x4*)(xrow + at + (u * 4 + fq) * 8) : u32x4{0u, 0u, 0u, 0u};
-#endif
 #pragma unroll
             for (u32 u = 0; u < U; u++)
 #pragma unroll

@@ -164,6 +164,12 @@ typedef struct hb_desc {
      * 144 KiB of x (one workgroup per CU, x staged once per CU), against
      * 64 KiB for 4. */
     uint32_t mv_waves;
+    /* MFMA GEMM (dense rows, direct-to-LDS): the K loop's schedule.  0: every
+     * wave loads and multiplies in lock step (wm x wn waves); 1: eight waves
+     * in two groups of four, one of each on every SIMD, taking turns between
+     * a memory phase and an MFMA phase (a "ping-pong"; wm * wn = 8, 3 or 4
+     * stages); 2: as 1 with the groups formed by even and odd waves. */
+    uint32_t sched;
 } hb_desc;
 
 /* Gpu::pipeline(&Emitted) (metal/gpu.rs:127-148) for the kernel the

@@ -102,3 +102,11 @@ def test_native_cli_usage_and_no_device():
         pytest.skip("a GPU is visible")
     r = subprocess.run([CLI, "64x128x256"], capture_output=True, text=True)
     assert r.returncode == 1 and "no HIP device" in r.stderr
+
+
+def test_shipped_library_has_no_development_hook():
+    """The shipped library reads no HB_DEV_DEFINES (only a development build
+    made by build.py --dev does): no environment variable can change what
+    its kernels compute."""
+    import herbert_hip as hb
+    assert b"HB_DEV_DEFINES" not in open(hb.LIB_PATH, "rb").read()
