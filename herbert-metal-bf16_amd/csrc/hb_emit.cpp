@@ -98,13 +98,14 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
             if (experts && (!d.top_k || !d.experts || !d.tiles))
                 return fail(HB_ERR_INVALID, "gemm over experts: top_k, experts and tiles");
             e->threads = 64 * d.wm * d.wn;
-            // LDS swizzle shift: 0 = the conflict-free one for gfx950's 64
-            // banks (256-byte lines hold 16/CH rows of CH chunks: rows
-            // r >> log2(16/CH) apart get distinct chunk slots); s+1 = s.
-            uint32_t ch = d.bk / 8, shift = 0;
+            // LDS swizzle shift: 0 = the conflict-free one on gfx950; s+1 =
+            // s.  The fragment reads (ds_read_b128, 16 rows at one chunk)
+            // measured conflict-free (SQ_LDS_BANK_CONFLICT = 0) with the chunk
+            // XORed by row >> 1 for rows of 4 and of 8 chunks (BK 32 and 64);
+            // row >> 2 for rows of 4 chunks conflicted on half of the LDS
+            // cycles.  Rows of 16 chunks: row >> 0.
+            uint32_t ch = d.bk / 8, shift = ch >= 16 ? 0 : 1;
             if (d.swz) shift = d.swz - 1;
-            else
-                for (uint32_t v = 16 / (ch < 16 ? ch : 16); v > 1; v >>= 1) shift++;
             std::string rows;
             if (d.rows_of == HB_ROWS_GATHER) {
                 snprintf(name, sizeof name, "_gather_k%u_t%u_m%u", d.top_k, d.tiles, d.bm);
@@ -120,19 +121,22 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
                 return fail(HB_ERR_UNSUPPORTED, "gemm: stages 1..4 (1..2 through registers)");
             if (d.w_nt > 1 || (d.w_nt && !d.lds_dma))
                 return fail(HB_ERR_UNSUPPORTED, "gemm: w_nt with direct-to-LDS staging");
-            if (d.sched > 2) return fail(HB_ERR_INVALID, "gemm: sched 0, 1 or 2");
-            if (d.sched && (swi || experts || !d.lds_dma || d.wm * d.wn != 8 || d.dbuf < 2 ||
-                            d.w_nt || ((d.bm * d.bk / 8) % 64) || ((d.bn * d.bk / 8) % 64) ||
-                            d.bm * d.bk / 8 / 64 / 8 + d.bn * d.bk / 8 / 64 / 8 == 0))
+            if (d.sched > 3) return fail(HB_ERR_INVALID, "gemm: sched 0..3");
+            if (d.sched && (swi || experts || !d.lds_dma || d.dbuf < 2 || d.w_nt ||
+                            d.wm * d.wn != (d.sched == 3 ? 4u : 8u) ||
+                            ((d.bm * d.bk / 8) % 64) || ((d.bn * d.bk / 8) % 64) ||
+                            (d.sched == 3 && (d.k / d.bk) % 2) ||
+                            (d.bm * d.bk / 8 / 64 + d.bn * d.bk / 8 / 64) < d.wm * d.wn))
                 return fail(HB_ERR_UNSUPPORTED,
-                            "gemm (ping-pong schedule): dense rows, direct-to-LDS, 8 waves, 3 or 4 "
-                            "stages, whole 1 KiB loads per stage, no w_nt");
+                            "gemm (pipelined schedules): dense rows, direct-to-LDS, 3 or 4 stages, "
+                            "8 waves (sched 1, 2) or 4 (sched 3, an even count of K tiles), whole "
+                            "1 KiB loads per stage, no w_nt");
             if (d.sched &&
                 (uint64_t)(d.dbuf + 1) * (d.bm + d.bn) * d.bk * 2 > 160 * 1024)
-                return fail(HB_ERR_UNSUPPORTED, "gemm (ping-pong schedule): stages beyond 160 KiB of LDS");
+                return fail(HB_ERR_UNSUPPORTED, "gemm (pipelined schedules): stages beyond 160 KiB of LDS");
             std::string band = d.band ? "_b" + std::to_string(d.band) : "";
             if (d.w_nt) band += "_wnt";
-            if (d.sched) band += d.sched == 1 ? "_pp" : "_pp2";
+            if (d.sched) band += d.sched == 1 ? "_pp" : d.sched == 2 ? "_pp2" : "_il";
             snprintf(name, sizeof name, "gemm_mma%s_%ux%u_%s%s_t%ux%u_k%u_w%ux%u_x%u_d%u%s_s%u_o%u%s%s",
                      swi ? "_swiglu" : "", d.k, d.n, out_tag(d.out), d.m_first ? "_mf" : "", d.bn,
                      d.bm, d.bk, d.wn, d.wm, d.mfma, d.dbuf, d.lds_dma ? "_dma" : "", shift, d.order,
@@ -149,7 +153,10 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
                           D("HB_ORDER", d.order), D("HB_MFIRST", d.m_first ? 1 : 0),
                           D("HB_DMA", d.lds_dma ? 1 : 0), D("HB_SWIGLU", swi ? 1 : 0),
                           D("HB_BAND", d.band), D("HB_W_NT", d.w_nt)};
-            if (d.sched) e->defines.push_back(D("HB_GRP", d.sched - 1));
+            if (d.sched) {
+                e->defines.push_back(D("HB_SCHED", d.sched == 3 ? 3 : 1));
+                e->defines.push_back(D("HB_GRP", d.sched == 2 ? 1 : 0));
+            }
             return HB_OK;
         }
         case HB_KIND_GEMM_SIMT:

@@ -232,7 +232,7 @@ struct Tune {
 // indexes this table (gemm.mma=1).
 struct Form {
     const char* name;
-    uint32_t bm, bn, bk, wm, wn, mfma, dbuf, dma, order, band;
+    uint32_t bm, bn, bk, wm, wn, mfma, dbuf, dma, order, band, sched;
 };
 const Form kForms[10] = {
     {"mma", 128, 128, 64, 2, 2, 16, 1, 1, 1},
@@ -272,6 +272,15 @@ const Form kMoreForms[] = {
     {"mma_t64x128", 64, 128, 64, 2, 2, 16, 2, 1, 1},
     {"mma_t64x64", 64, 64, 64, 2, 2, 16, 2, 1, 1},
     {"mma_t32x64", 32, 64, 64, 1, 4, 16, 2, 1, 1},
+    // Eight waves in two groups taking turns between memory and MFMA phases
+    // (hb_desc.sched 1), four stages of 32 K: 256 x 288 tiles fill exactly
+    // two rounds of the CUs on 2048 x 18432 (and 4608: 128 tiles).
+    {"pp_t256x288", 256, 288, 32, 4, 2, 16, 3, 1, 1, 0, 1},
+    {"pp_t256x256", 256, 256, 32, 4, 2, 16, 3, 1, 1, 0, 1},
+    {"pp_t256x192", 256, 192, 32, 4, 2, 16, 3, 1, 1, 0, 1},
+    {"pp_t256x128", 256, 128, 32, 4, 2, 16, 3, 1, 1, 0, 1},
+    {"pp_t128x256", 128, 256, 32, 2, 4, 16, 3, 1, 1, 0, 1},
+    {"pp_t128x128", 128, 128, 32, 2, 4, 16, 3, 1, 1, 0, 1},
 };
 // The fused [gate | up] + SwiGLU forms (gate_up_pipes, qwen.rs:2148-2193):
 // bn W rows per tile = bn/2 features.
@@ -300,6 +309,7 @@ hb_desc form_desc(const Form& f, uint32_t k, uint32_t n, uint32_t out, bool mf) 
     d.lds_dma = f.dma;
     d.order = f.order;
     d.band = f.band;
+    d.sched = f.sched;
     return d;
 }
 
@@ -619,6 +629,33 @@ int hb_engine_log_summary(hb_engine* e) {
     return HB_OK;
 }
 
+// The dense GEMM candidates of QwenEngine::gemm's timed choice, in order
+// (qwen.rs:2200-2325): the gemm.mform table (its first the production
+// kernel every other is checked against), the further tile forms, the
+// direct MFMA forms (gemm_mm2d), then candidates a caller added.
+std::vector<std::pair<std::string, hb_desc>> gemm_candidates(hb_engine* e, uint32_t k, uint32_t n,
+                                                             uint32_t out, bool mf) {
+    std::vector<std::pair<std::string, hb_desc>> v;
+    for (const auto& f : kForms) v.emplace_back(f.name, form_desc(f, k, n, out, mf));
+    for (const auto& f : kMoreForms) v.emplace_back(f.name, form_desc(f, k, n, out, mf));
+    for (auto tm_tn : {std::make_pair(64u, 64u), std::make_pair(64u, 32u), std::make_pair(32u, 64u),
+                       std::make_pair(32u, 32u), std::make_pair(64u, 16u), std::make_pair(32u, 16u)}) {
+        char nm[32];
+        snprintf(nm, sizeof nm, "mm2d%ux%u", tm_tn.first, tm_tn.second);
+        v.emplace_back(nm, mm2d_desc(k, n, out, mf, tm_tn.first, tm_tn.second));
+    }
+    for (const auto& ex : e->extra) v.push_back(ex);
+    return v;
+}
+
+int hb_engine_gemm_candidates(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, hb_desc* descs,
+                              uint32_t cap, uint32_t* count) {
+    const auto v = gemm_candidates(e, k, n, out, e->t["gemm.mfirst"] != 0);
+    *count = (uint32_t)v.size();
+    for (uint32_t i = 0; i < v.size() && i < cap; i++) descs[i] = v[i].second;
+    return HB_OK;
+}
+
 int hb_engine_gemm(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, hb_range state,
                    hb_range w, hb_range x, hb_range y, uint32_t m, int32_t* kernel) {
     const Tune& t = e->t;
@@ -669,19 +706,11 @@ int hb_engine_gemm(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, hb_range 
         c.push_back({name, kk, {make_op(kk, m, {state, w, x, y, state, state})}});
         eligible.push_back(true);
     };
-    for (const auto& f : kForms) add(f.name, form_desc(f, k, n, out, mf));
-    if (c.empty() || (!big && c[0].name != "mma"))
-        return fail(HB_ERR_COMPILE, what + ": the production kernel mma is not built: " + hb_last_error());
-    for (const auto& f : kMoreForms) add(f.name, form_desc(f, k, n, out, mf));
-    for (auto tm_tn : {std::make_pair(64u, 64u), std::make_pair(64u, 32u), std::make_pair(32u, 64u),
-                       std::make_pair(32u, 32u), std::make_pair(64u, 16u), std::make_pair(32u, 16u)}) {
-        char nm[32];
-        snprintf(nm, sizeof nm, "mm2d%ux%u", tm_tn.first, tm_tn.second);
-        add(nm, mm2d_desc(k, n, out, mf, tm_tn.first, tm_tn.second));
-    }
-    for (const auto& ex : e->extra) {
-        hb_desc d = ex.second;
-        add(ex.first, d);
+    const auto list = gemm_candidates(e, k, n, out, mf);
+    for (size_t i = 0; i < list.size(); i++) {
+        add(list[i].first, list[i].second);
+        if (i + 1 == sizeof kForms / sizeof kForms[0] && (c.empty() || (!big && c[0].name != "mma")))
+            return fail(HB_ERR_COMPILE, what + ": the production kernel mma is not built: " + hb_last_error());
     }
     uint32_t row_bytes = n * (out == HB_OUT_F32 ? 4 : 2);
     if ((rc = e->check_candidates(what, c, eligible, state, y, out == HB_OUT_F32, m, row_bytes))) return rc;

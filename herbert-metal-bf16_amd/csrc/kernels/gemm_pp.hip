@@ -1,6 +1,10 @@
-// gemm_pp.hip -- the prefill block GEMM with two groups of wavefronts that
-// take turns on the matrix cores: Y[m][N] = X[m][K] . W[N][K]^T, bf16
-// operands, f32 accumulators, one rounding at the output as Out says.
+// gemm_pp.hip -- the prefill block GEMM with its K loop software-pipelined
+// across or within wavefronts: Y[m][N] = X[m][K] . W[N][K]^T, bf16 operands,
+// f32 accumulators, one rounding at the output as Out says.  Two schedules
+// (HB_SCHED): 1, two groups of four wavefronts that take turns on the matrix
+// cores ("ping-pong"); 3, four wavefronts, one per SIMD, each issuing its
+// next K tile's LDS reads between its MFMAs (larger wave tiles: fewer LDS
+// bytes per flop).
 //
 // Reference: src/metal/prefill.rs:838-1307 (gemm_mma_rows / gemm_mma_impl:
 // the staged K loop at :1177-1192, the clamped rows, the epilogue of Out at
@@ -29,6 +33,16 @@
 //  issued NS - 1 tiles ahead (three with four stages), so the L2/HBM latency
 //  is covered by about 2 * (NS - 1) phases of MFMA work.
 //
+// HB_SCHED 3 (four waves, wave tiles of TM x TN, two fragment register sets):
+//   barrier B_k | loads of K tile k + NS into stage k % NS;
+//               | MFMAs of tile k (fragments in set k % 2) interleaved with
+//               |   the LDS reads of tile k + 1's fragments into set 1 - k % 2;
+//               | own loads of tile k + 2 landed, LDS reads done | B_{k+1}
+//  Stage k % NS is free at B_k: tile k's fragments were read during step k-1
+//  and every wave waited for those reads before B_k.  Tile k + 1 is visible
+//  at B_k: every wave waited for its own loads of it at the end of step k-1.
+//  Loads run NS - 1 steps ahead of the barrier that needs them.
+//
 // Ordering (phase p = the span between two barriers; A runs MEM(k) in phase
 // 2k and COMP(k) in 2k+1, B one phase later):
 //  - the stage MEM(k) loads into was last read in MEM(k-1), i.e. by A in
@@ -48,8 +62,9 @@
 //
 // Compile-time constants (-D): HB_K, HB_N, HB_OUT (0 bf16, 1 f32, 2
 // residual), HB_BM, HB_BN, HB_BK, HB_WM, HB_WN (WM * WN = 8), HB_MFMA (16|32),
-// HB_STAGES (3|4), HB_SWZ, HB_ORDER, HB_MFIRST, HB_BAND, HB_GRP (which waves
-// form a group: 0 waves 0-3 / 4-7, 1 even / odd waves).
+// HB_STAGES (3|4), HB_SWZ, HB_ORDER, HB_MFIRST, HB_BAND, HB_SCHED (1 | 3),
+// HB_GRP (ping-pong: which waves form a group: 0 waves 0-3 / 4-7, 1 even /
+// odd waves).
 //
 // Bindings: state (u32[4], state[3] = rows), W, X, Y, list, tiles (unused:
 // dense rows); then the rows the launch was sized for (m_launch).
@@ -58,7 +73,11 @@
 constexpr u32 K = HB_K, N = HB_N;
 constexpr int OUT = HB_OUT;
 constexpr u32 BM = HB_BM, BN = HB_BN, BK = HB_BK;
-constexpr u32 WM = HB_WM, WN = HB_WN, NT = 512;
+#ifndef HB_SCHED
+#define HB_SCHED 1
+#endif
+constexpr bool PP = HB_SCHED == 1;
+constexpr u32 WM = HB_WM, WN = HB_WN, NWV = PP ? 8 : 4, NT = 64 * NWV;
 constexpr u32 FM = HB_MFMA;
 constexpr u32 TM = BM / WM, TN = BN / WN;
 constexpr u32 IM = TM / FM, IN = TN / FM;
@@ -70,11 +89,11 @@ constexpr u32 NS = HB_STAGES;
 constexpr u32 NTILES = (N + BN - 1) / BN;
 constexpr u32 XST = BM * CH, WST = BN * CH;  // chunks per stage
 // Wave-loads (64 chunks, 1 KiB) per stage of each operand, shared out over
-// the 8 waves: wave w issues the operand's wave-loads w, w + 8, ...; when a
-// count is not a multiple of 8 the first waves issue one more.
+// the NWV waves: wave w issues the operand's wave-loads w, w + NWV, ...; when
+// a count is not a multiple of NWV the first waves issue one more.
 constexpr u32 NXL = XST / 64, NWL = WST / 64;
-constexpr u32 XLMAX = (NXL + 7) / 8, WLMAX = (NWL + 7) / 8;
-constexpr u32 LMIN = NXL / 8 + NWL / 8;  // loads per stage of every wave
+constexpr u32 XLMAX = (NXL + NWV - 1) / NWV, WLMAX = (NWL + NWV - 1) / NWV;
+constexpr u32 LMIN = NXL / NWV + NWL / NWV;  // loads per stage of every wave
 #ifndef HB_BAND
 #define HB_BAND 0
 #endif
@@ -82,13 +101,15 @@ constexpr u32 LMIN = NXL / 8 + NWL / 8;  // loads per stage of every wave
 #define HB_GRP 0
 #endif
 
-static_assert(WM * WN == 8, "eight wavefronts");
+static_assert(HB_SCHED == 1 || HB_SCHED == 3, "schedule 1 or 3");
+static_assert(WM * WN == NWV, "eight wavefronts (ping-pong) or four");
 static_assert(K % BK == 0, "K a multiple of the K step");
 static_assert(N % 4 == 0, "N a multiple of 4");
 static_assert(TM % FM == 0 && TN % FM == 0, "wave tile a multiple of the MFMA block");
 static_assert(BK % KS == 0 && (CH & (CH - 1)) == 0, "K step");
 static_assert(XST % 64 == 0 && WST % 64 == 0, "whole wave-loads per stage");
 static_assert(NS >= 3 && NS <= 4, "3 or 4 stages");
+static_assert(PP || KT % 2 == 0, "four-wave schedule: an even count of K tiles");
 static_assert(LMIN >= 1, "every wave loads");
 
 typedef __attribute__((ext_vector_type(FM == 16 ? 4 : 16))) float acc_t;
@@ -130,6 +151,7 @@ HB_DEV void store4(void* Yv, u64 at, float v0, float v1, float v2, float v3) {
 }
 
 #define HB_INLINE __attribute__((always_inline))
+template <bool B> struct bconst { static constexpr bool value = B; };
 
 extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     const u32* __restrict__ state, const u16* __restrict__ W, const u16* __restrict__ X,
@@ -180,13 +202,13 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     u32 xoff[XLMAX], woff[WLMAX];
 #pragma unroll
     for (u32 i = 0; i < XLMAX; i++) {
-        const u32 p = (wave + 8 * i) * 64 + lane, r = p / CH;
+        const u32 p = (wave + NWV * i) * 64 + lane, r = p / CH;
         const u32 cc = (p % CH) ^ ((r >> HB_SWZ) & (CH - 1));
         xoff[i] = r < rows && r < BM ? ((row0 + r) * K + cc * 8) * 2 : 0x80000000u;
     }
 #pragma unroll
     for (u32 i = 0; i < WLMAX; i++) {
-        const u32 p = (wave + 8 * i) * 64 + lane, r = p / CH;
+        const u32 p = (wave + NWV * i) * 64 + lane, r = p / CH;
         const u32 cc = (p % CH) ^ ((r >> HB_SWZ) & (CH - 1));
         const u32 n = n0 + r;
         woff[i] = ((n < N ? n : N - 1) * K + cc * 8) * 2;
@@ -199,21 +221,21 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     typedef __attribute__((address_space(3))) u32x4 lds_u32x4;
     auto lds_addr = [&](u32x4* p) HB_INLINE -> u32 { return (u32)(u64)(lds_u32x4*)p; };
     // This wave's loads of K tile kt into stage st (the branches are
-    // wave-uniform and only where a count is not a multiple of 8).
+    // wave-uniform and only where a count is not a multiple of NWV).
     auto load_tile = [&](u32 kt, u32 st) HB_INLINE {
         const u32 kb = kt * BK * 2;
 #pragma unroll
         for (u32 i = 0; i < XLMAX; i++) {
-            if (NXL % 8 && wave + 8 * i >= NXL) continue;
+            if (NXL % NWV && wave + NWV * i >= NXL) continue;
             asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                         :: "s"(lds_addr(&sXa[st * XST + (wave + 8 * i) * 64])), "v"(xoff[i]),
+                         :: "s"(lds_addr(&sXa[st * XST + (wave + NWV * i) * 64])), "v"(xoff[i]),
                             "s"(rX), "s"(kb) : "memory");
         }
 #pragma unroll
         for (u32 i = 0; i < WLMAX; i++) {
-            if (NWL % 8 && wave + 8 * i >= NWL) continue;
+            if (NWL % NWV && wave + NWV * i >= NWL) continue;
             asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-                         :: "s"(lds_addr(&sWa[st * WST + (wave + 8 * i) * 64])), "v"(woff[i]),
+                         :: "s"(lds_addr(&sWa[st * WST + (wave + NWV * i) * 64])), "v"(woff[i]),
                             "s"(rW), "s"(kb) : "memory");
         }
     };
@@ -232,8 +254,9 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
                   "fragment rows keep the lane's swizzle");
     const u32 fsw = (fr >> HB_SWZ) & (CH - 1);
     const u32 wbase = (wn * TN + fr) * CH, xbase = (wm * TM + fr) * CH;
-    bf16x8 a[S][IN], b[S][IM];
-    auto read_frags = [&](u32 st) HB_INLINE {
+    constexpr u32 NF = PP ? 1 : 2;  // fragment register sets
+    bf16x8 a[NF][S][IN], b[NF][S][IM];
+    auto read_frags = [&](u32 st, u32 h) HB_INLINE {
         const u32x4* sW = sWa + st * WST;
         const u32x4* sX = sXa + st * XST;
 #pragma unroll
@@ -241,23 +264,22 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
             const u32 ch = (s * (KS / 8) + fc) ^ fsw;
 #pragma unroll
             for (u32 i = 0; i < IN; i++)
-                a[s][i] = __builtin_bit_cast(bf16x8, sW[wbase + ch + i * FM * CH]);
+                a[h][s][i] = __builtin_bit_cast(bf16x8, sW[wbase + ch + i * FM * CH]);
 #pragma unroll
             for (u32 j = 0; j < IM; j++)
-                b[s][j] = __builtin_bit_cast(bf16x8, sX[xbase + ch + j * FM * CH]);
+                b[h][s][j] = __builtin_bit_cast(bf16x8, sX[xbase + ch + j * FM * CH]);
         }
     };
-    auto compute = [&]() HB_INLINE {
-        __builtin_amdgcn_s_setprio(1);
+    auto compute = [&](u32 h) HB_INLINE {
 #pragma unroll
         for (u32 s = 0; s < S; s++)
 #pragma unroll
             for (u32 i = 0; i < IN; i++)
 #pragma unroll
-                for (u32 j = 0; j < IM; j++) acc[i][j] = mfma(a[s][i], b[s][j], acc[i][j]);
-        __builtin_amdgcn_s_setprio(0);
+                for (u32 j = 0; j < IM; j++) acc[i][j] = mfma(a[h][s][i], b[h][s][j], acc[i][j]);
     };
 
+    if constexpr (PP) {
     // Prologue: K tiles 0..NS-2 in flight, this wave's share of tile 0
     // landed, then the barrier that publishes tile 0.
 #pragma unroll
@@ -274,14 +296,16 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
         __builtin_amdgcn_sched_barrier(0);
         const bool more = kt + NS - 1 < KT;
         if (more) load_tile(kt + NS - 1, st == 0 ? NS - 1 : st - 1);
-        read_frags(st);
+        read_frags(st, 0);
         // Own loads of K tile kt + 1 landed: at most the later tiles' loads
         // (LMIN or more each) still in flight.
         if (more) WAIT_VM((NS - 2) * LMIN);
         else WAIT_VM(0);
         PHASE_END_LDS();
         __builtin_amdgcn_sched_barrier(0);
-        compute();
+        __builtin_amdgcn_s_setprio(1);
+        compute(0);
+        __builtin_amdgcn_s_setprio(0);
         __builtin_amdgcn_sched_barrier(0);
         PHASE_END();
     };
@@ -299,6 +323,59 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     }
     // Group A meets group B's last barrier: equal barrier counts.
     if (grp == 0) PHASE_END();
+    } else {
+    // Four waves.  Prologue: every stage's K tile in flight, tile 0 landed
+    // and published, its fragments read, tile 1 landed and published (B_0).
+#pragma unroll
+    for (u32 t = 0; t < NS; t++)
+        if (t < KT) load_tile(t, t);
+    if (KT >= NS) WAIT_VM((NS - 1) * LMIN);
+    else WAIT_VM(0);
+    PHASE_END();
+    read_frags(0, 0);
+    if (KT >= NS) WAIT_VM((NS - 2) * LMIN);
+    else WAIT_VM(0);
+    PHASE_END_LDS();
+    // Step kt (stage st, fragment set h): one LDS read, then a few MFMAs,
+    // in turn (scheduling groups), the loads first.  `next`: a K tile
+    // follows (its fragments are read during this step).
+    auto step = [&](u32 kt, u32 st, u32 h, auto next) HB_INLINE {
+        __builtin_amdgcn_sched_barrier(0);
+        const bool more = kt + NS < KT;
+        if (more) load_tile(kt + NS, st);
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (decltype(next)::value) {
+            read_frags(st + 1 == NS ? 0 : st + 1, 1 - h);
+            compute(h);
+            constexpr u32 NR = S * (IN + IM), NM = S * IN * IM, PER = NM / NR ? NM / NR : 1;
+#pragma unroll
+            for (u32 q = 0; q < NR; q++) {
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+                __builtin_amdgcn_sched_group_barrier(0x008, PER, 0);  // MFMA
+            }
+        } else {
+            compute(h);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // Own loads of tile kt + 2 landed: at most NS - 2 later tiles' loads
+        // still in flight.
+        if (more) WAIT_VM((NS - 2) * LMIN);
+        else WAIT_VM(0);
+        PHASE_END_LDS();
+    };
+    // K tiles in pairs (fragment sets 0, 1), the last pair apart: its second
+    // step reads no next tile.
+    u32 st = 0;
+    for (u32 kt = 0; kt + 2 < KT; kt += 2) {
+        step(kt, st, 0, bconst<true>{});
+        st = st + 1 == NS ? 0 : st + 1;
+        step(kt + 1, st, 1, bconst<true>{});
+        st = st + 1 == NS ? 0 : st + 1;
+    }
+    step(KT - 2, st, 0, bconst<true>{});
+    st = st + 1 == NS ? 0 : st + 1;
+    step(KT - 1, st, 1, bconst<false>{});
+    }
 
     // Epilogue: per MFMA block, runs of 4 columns of one row.
 #pragma unroll

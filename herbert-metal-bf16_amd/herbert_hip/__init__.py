@@ -459,6 +459,14 @@ class Engine:
     def add_gemm_candidate(self, name, desc):
         check(lib.hb_engine_add_gemm_candidate(self.h, name.encode(), ctypes.byref(desc)))
 
+    def gemm_candidates(self, k, n, out):
+        """The descriptors gemm() times for a k x n GEMM, in candidate order."""
+        cap = 256
+        arr = (Desc * cap)()
+        cnt = _u32()
+        check(lib.hb_engine_gemm_candidates(self.h, k, n, int(out), arr, cap, ctypes.byref(cnt)))
+        return [arr[i].replace() for i in range(min(cnt.value, cap))]
+
     def gemm(self, k, n, out, state, w, x, y, m):
         kern = _i32()
         check(lib.hb_engine_gemm(self.h, k, n, int(out), state, w, x, y, m, ctypes.byref(kern)))

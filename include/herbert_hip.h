@@ -168,7 +168,10 @@ typedef struct hb_desc {
      * wave loads and multiplies in lock step (wm x wn waves); 1: eight waves
      * in two groups of four, one of each on every SIMD, taking turns between
      * a memory phase and an MFMA phase (a "ping-pong"; wm * wn = 8, 3 or 4
-     * stages); 2: as 1 with the groups formed by even and odd waves. */
+     * stages); 2: as 1 with the groups formed by even and odd waves; 3: four
+     * waves (wm * wn = 4), one per SIMD, each reading its next K tile's
+     * fragments from LDS between its MFMAs (3 or 4 stages, an even count of
+     * K tiles). */
     uint32_t sched;
 } hb_desc;
 
@@ -255,6 +258,14 @@ int hb_engine_buckets(hb_engine *engine, uint32_t *out, uint32_t cap, uint32_t *
  * timed on (state[3] and Y restored afterwards).  Logs [autotune] lines. */
 int hb_engine_gemm(hb_engine *engine, uint32_t k, uint32_t n, uint32_t out, hb_range state,
                    hb_range w, hb_range x, hb_range y, uint32_t m, int32_t *kernel);
+
+/* The descriptors QwenEngine::gemm (qwen.rs:2200-2325) times for a k x n
+ * GEMM written as `out`, in candidate order (the first is the production
+ * kernel the others are checked against); *count = how many, the first
+ * min(count, cap) written.  Lets a caller check or build every kernel the
+ * timed choice can pick. */
+int hb_engine_gemm_candidates(hb_engine *engine, uint32_t k, uint32_t n, uint32_t out,
+                              hb_desc *descs, uint32_t cap, uint32_t *count);
 
 /* QwenEngine::gate_up_pipes (qwen.rs:2148-2193): the prefill's [gate | up]
  * GEMM (K = h, N = 2*inter, Bf16 into `gu`) and its SwiGLU into `hout`

@@ -33,6 +33,21 @@ TILES = {
                                band=4),
     "t128x160_s4_b4": dict(bm=128, bn=160, bk=64, wm=2, wn=2, mfma=16, dbuf=3, lds_dma=1, order=1, band=4),
     "t32x64_s3": dict(bm=32, bn=64, bk=64, wm=1, wn=4, mfma=16, dbuf=2, lds_dma=1, order=1),
+    # the ping-pong schedule (hb_desc.sched 1, 2: two wave groups taking turns)
+    "pp_t256x288": dict(bm=256, bn=288, bk=32, wm=4, wn=2, mfma=16, dbuf=3, lds_dma=1, order=1, sched=1),
+    "pp_t256x256_b4": dict(bm=256, bn=256, bk=32, wm=4, wn=2, mfma=16, dbuf=3, lds_dma=1, order=1,
+                           band=4, sched=1),
+    "pp_t128x128": dict(bm=128, bn=128, bk=32, wm=2, wn=4, mfma=16, dbuf=3, lds_dma=1, order=1, sched=1),
+    "pp_t128x256_s3": dict(bm=128, bn=256, bk=32, wm=2, wn=4, mfma=16, dbuf=2, lds_dma=1, order=0,
+                           sched=1),
+    "pp_t256x192_x32_g2": dict(bm=256, bn=192, bk=32, wm=4, wn=2, mfma=32, dbuf=3, lds_dma=1, order=1,
+                               sched=2),
+    "pp_t256x160_k64": dict(bm=256, bn=160, bk=64, wm=4, wn=2, mfma=16, dbuf=2, lds_dma=1, order=1,
+                            sched=1),
+    # four waves, each reading its next K tile between its MFMAs (sched 3)
+    "il_t256x256": dict(bm=256, bn=256, bk=32, wm=2, wn=2, mfma=16, dbuf=3, lds_dma=1, order=1, sched=3),
+    "il_t256x192_s3": dict(bm=256, bn=192, bk=32, wm=2, wn=2, mfma=16, dbuf=2, lds_dma=1, order=1,
+                           sched=3),
 }
 
 
