@@ -145,6 +145,10 @@ HB_DEV void store4(void* Yv, u64 at, float v0, float v1, float v2, float v3) {
     }
 }
 
+#include "gemm_epi.h"
+// Dense rows through direct-to-LDS stages: the epilogue through LDS.
+constexpr bool EPI_VIA_LDS = EPI_LDS && HB_DMA && ROWS == 0 && !SWI;
+
 #define HB_INLINE __attribute__((always_inline))
 
 extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
@@ -154,7 +158,10 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
 #if HB_DMA
     // The stages, one after another in one LDS array per operand; the stage
     // in use is a scalar index, so any count of K tiles runs one loop body.
-    __shared__ u32x4 sXa[NS * XCHP], sWa[NS * WCHP];
+    constexpr u32 STG = NS * (XCHP + WCHP), EPC = EPI_VIA_LDS ? EPI_CHUNKS : 0;
+    __shared__ u32x4 lds[STG > EPC ? STG : EPC];
+    u32x4* const sXa = lds;
+    u32x4* const sWa = lds + NS * XCHP;
 #else
     // Register staging: the stages as distinct LDS objects, so that the
     // compiler sees that one stage's stores never alias the other's reads.
@@ -477,6 +484,12 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     }
 #endif
 
+#if HB_DMA
+    if constexpr (EPI_VIA_LDS) {
+        epilogue_lds(lds, acc, tid, wm, wn, fr, fc, row0, rows, n0, Yv);
+        return;
+    }
+#endif
     // Epilogue: lane holds, per MFMA block, runs of 4 columns of one row.
 #pragma unroll
     for (u32 j = 0; j < IM; j++) {

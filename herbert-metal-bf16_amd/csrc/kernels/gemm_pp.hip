@@ -150,6 +150,8 @@ HB_DEV void store4(void* Yv, u64 at, float v0, float v1, float v2, float v3) {
     }
 }
 
+#include "gemm_epi.h"
+
 #define HB_INLINE __attribute__((always_inline))
 template <bool B> struct bconst { static constexpr bool value = B; };
 
@@ -159,7 +161,11 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     u32 m_launch) {
     (void)list;
     (void)tiles;
-    __shared__ u32x4 sXa[NS * XST], sWa[NS * WST];
+    // The stages, X's then W's; after the K loop the epilogue's staging.
+    constexpr u32 STG = NS * (XST + WST);
+    __shared__ u32x4 lds[STG > EPI_CHUNKS ? STG : EPI_CHUNKS];
+    u32x4* const sXa = lds;
+    u32x4* const sWa = lds + NS * XST;
 
     const u32 tid = threadIdx.x, lane = tid & 63u;
     const u32 wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -377,7 +383,12 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     step(KT - 1, st, 1, bconst<false>{});
     }
 
-    // Epilogue: per MFMA block, runs of 4 columns of one row.
+    if constexpr (EPI_LDS) {
+        epilogue_lds(lds, acc, tid, wm, wn, fr, fc, row0, rows, n0, Yv);
+        return;
+    }
+    // Epilogue (F32, or N not a multiple of 8): per MFMA block, runs of 4
+    // columns of one row.
 #pragma unroll
     for (u32 j = 0; j < IM; j++) {
         const u32 ml = wm * TM + j * FM + fr;
