@@ -281,6 +281,13 @@ const Form kMoreForms[] = {
     {"pp_t256x128", 256, 128, 32, 4, 2, 16, 3, 1, 1, 0, 1},
     {"pp_t128x256", 128, 256, 32, 2, 4, 16, 3, 1, 1, 0, 1},
     {"pp_t128x128", 128, 128, 32, 2, 4, 16, 3, 1, 1, 0, 1},
+    // One round of tiles on the narrower layer shapes: 256 x 160 on 2048 x
+    // 4608 (232 tiles), 128 x 160 on 2048 x 2560 (256), three or four
+    // stages of 64 K (longer MFMA phases than 32 K at these wave tiles).
+    {"pp_t256x160_k64", 256, 160, 64, 4, 2, 16, 2, 1, 1, 0, 1},
+    {"pp_t128x160_k64", 128, 160, 64, 4, 2, 16, 3, 1, 1, 0, 1},
+    {"pp_t128x160_k64_b4", 128, 160, 64, 4, 2, 16, 3, 1, 1, 4, 1},
+    {"pp_t128x288_k64", 128, 288, 64, 4, 2, 16, 2, 1, 1, 0, 1},
 };
 // The fused [gate | up] + SwiGLU forms (gate_up_pipes, qwen.rs:2148-2193):
 // bn W rows per tile = bn/2 features.

@@ -44,6 +44,8 @@ TILES = {
                                sched=2),
     "pp_t256x160_k64": dict(bm=256, bn=160, bk=64, wm=4, wn=2, mfma=16, dbuf=2, lds_dma=1, order=1,
                             sched=1),
+    "pp_t128x160_k64_b4": dict(bm=128, bn=160, bk=64, wm=4, wn=2, mfma=16, dbuf=3, lds_dma=1, order=1,
+                               band=4, sched=1),
     # four waves, each reading its next K tile between its MFMAs (sched 3)
     "il_t256x256": dict(bm=256, bn=256, bk=32, wm=2, wn=2, mfma=16, dbuf=3, lds_dma=1, order=1, sched=3),
     "il_t256x192_s3": dict(bm=256, bn=192, bk=32, wm=2, wn=2, mfma=16, dbuf=2, lds_dma=1, order=1,
