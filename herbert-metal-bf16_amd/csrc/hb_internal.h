@@ -81,4 +81,15 @@ struct hb_gpu {
 namespace hb {
 // Resolves a range to a device pointer and byte size (size 0 = to the end).
 int resolve(hb_gpu* g, const hb_range& r, char** ptr, uint64_t* size);
+// hb_launch over device pointers and their byte sizes (checked against the
+// kernel's descriptor and m first).
+int launch_ptrs(hb_gpu* g, int32_t kernel, void* const* ptrs, const uint64_t* sizes, uint32_t nbind,
+                uint32_t m);
+// The descriptor a kernel was built from (defaults filled), or null.
+const hb_desc* kernel_desc(hb_gpu* g, int32_t kernel);
+// The routed experts of an MoE layer over device pointers (hb_moe.cpp):
+// bindings in hb_moe_io's order (state, route, list, tiles, x, w_gate_up,
+// egu, ehb, w_down, ey, xs), then out.
+int moe_experts_run(hb_gpu* g, const int32_t kernels[4], int32_t swiglu, int32_t combine,
+                    void* const ptr[12], const uint64_t size[12], uint32_t m);
 }  // namespace hb

@@ -188,13 +188,28 @@ static int launch_raw(hb_gpu* g, const Kernel& k, void** ptrs, uint32_t nptr, ui
     return HB_OK;
 }
 
-static int launch(hb_gpu* g, int32_t kernel, const hb_range* b, uint32_t nbind, uint32_t m) {
+int launch_ptrs(hb_gpu* g, int32_t kernel, void* const* ptrs, const uint64_t* sizes, uint32_t nbind,
+                uint32_t m) {
     if (kernel < 0 || (size_t)kernel >= g->kernels.size())
         return fail(HB_ERR_INVALID, "no kernel " + std::to_string(kernel));
     const Kernel& k = g->kernels[kernel];
     if (nbind != k.em.nbind)
         return fail(HB_ERR_INVALID, k.em.name + ": " + std::to_string(nbind) +
                                         " bindings given, it takes " + std::to_string(k.em.nbind));
+    int rc = check_bindings(k.desc, sizes, nbind, m);
+    if (rc) return fail(rc, k.em.name + ": " + hb_last_error());
+    void* p[10];
+    for (uint32_t i = 0; i < nbind; i++) p[i] = ptrs[i];
+    return launch_raw(g, k, p, nbind, m, groups_of(k.desc, m));
+}
+
+const hb_desc* kernel_desc(hb_gpu* g, int32_t kernel) {
+    if (kernel < 0 || (size_t)kernel >= g->kernels.size()) return nullptr;
+    return &g->kernels[kernel].desc;
+}
+
+static int launch(hb_gpu* g, int32_t kernel, const hb_range* b, uint32_t nbind, uint32_t m) {
+    if (nbind > 10) return fail(HB_ERR_INVALID, "more than 10 bindings");
     void* ptrs[10];
     uint64_t sizes[10];
     for (uint32_t i = 0; i < nbind; i++) {
@@ -203,9 +218,7 @@ static int launch(hb_gpu* g, int32_t kernel, const hb_range* b, uint32_t nbind, 
         if (rc) return rc;
         ptrs[i] = p;
     }
-    int rc = check_bindings(k.desc, sizes, nbind, m);
-    if (rc) return fail(rc, k.em.name + ": " + hb_last_error());
-    return launch_raw(g, k, ptrs, nbind, m, groups_of(k.desc, m));
+    return launch_ptrs(g, kernel, ptrs, sizes, nbind, m);
 }
 
 }  // namespace hb
@@ -345,20 +358,16 @@ int hb_zero(hb_gpu* g, hb_buf buf, uint64_t offset, uint64_t bytes) {
         if (rc) return rc;
         g->zero_built = true;
     }
-    // Whole 16-byte words by the kernel, a ragged head or tail by copies.
-    uint64_t words = n / 16;
-    if (words) {
-        void* ptrs[2] = {p, nullptr};
-        uint32_t groups = (uint32_t)((words + 255) / 256);
-        if (words > 0xffffffffull || groups > 0x7fffffffu)
-            return fail(HB_ERR_INVALID, "hb_zero: too large");
-        void* args[3] = {&ptrs[0], &words, nullptr};
-        HB_HIP(hipModuleLaunchKernel(g->zero_kernel.fn, groups, 1, 1, 256, 1, 1, 0, g->stream,
-                                     args, nullptr));
-    }
-    if (n % 16) {
-        static const char zeros[16] = {0};
-        HB_HIP(hipMemcpyAsync(p + words * 16, zeros, n % 16, hipMemcpyHostToDevice, g->stream));
+    // One thread per 16-byte-aligned word of the span; the kernel zeroes a
+    // ragged first or last word byte by byte.
+    if (n) {
+        const uint64_t words = (((uint64_t)p + n + 15) >> 4) - ((uint64_t)p >> 4);
+        const uint64_t groups = (words + 255) / 256;
+        if (groups > 0x7fffffffull) return fail(HB_ERR_INVALID, "hb_zero: too large");
+        void* ptr = p;
+        void* args[2] = {&ptr, &n};
+        HB_HIP(hipModuleLaunchKernel(g->zero_kernel.fn, (uint32_t)groups, 1, 1, 256, 1, 1, 0,
+                                     g->stream, args, nullptr));
     }
     return HB_OK;
 }

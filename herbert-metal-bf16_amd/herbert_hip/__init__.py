@@ -198,6 +198,10 @@ lib.hb_engine_matvec_fused.argtypes = [_P, _u32, _u32, _u32, _u32, _u32, _u32, _
                                        ctypes.POINTER(_i32)]
 lib.hb_engine_experts.argtypes = [_P, _u32, _u32, _u32, _u32, _u32, ctypes.POINTER(MoeIo),
                                   ctypes.POINTER(_i32), ctypes.POINTER(_u32)]
+lib.hb_engine_gemm_candidates.argtypes = [_P, _u32, _u32, _u32, ctypes.POINTER(Desc), _u32,
+                                          ctypes.POINTER(_u32)]
+lib.hb_moe_experts_run.argtypes = [_P, ctypes.POINTER(_i32), _i32, _i32, ctypes.POINTER(MoeIo), Range,
+                                   _u32]
 lib.hb_engine_autotune_seconds.argtypes = [_P]
 lib.hb_engine_autotune_seconds.restype = ctypes.c_double
 
@@ -575,6 +579,16 @@ class MoeLayer:
                            r(b["tiles"])], m))
         ops.append(Op(self.combine_k, [r(b["ey"]), r(b["route"]), r(b["out"])], m))
         return ops
+
+    def run(self, m=None):
+        """The layer in two host calls: route_qwen, then hb_moe_experts_run
+        (the rest of ops() as one native dispatch sequence)."""
+        m = self.rows if m is None else m
+        b = self.buf
+        self.gpu.launch(self.route_k, [r(b["scores"]), r(b["route"])], m)
+        ks = (ctypes.c_int32 * 4)(*self.kernels)
+        check(lib.hb_moe_experts_run(self.gpu.h, ks, self.swiglu_k, self.combine_k,
+                                     ctypes.byref(self.io), r(b["out"]), m))
 
     def free(self):
         for name, buf in self.buf.items():

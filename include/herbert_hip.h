@@ -318,6 +318,19 @@ int hb_engine_experts(hb_engine *engine, uint32_t experts, uint32_t top_k, uint3
                       uint32_t inter, uint32_t m, const hb_moe_io *io, int32_t kernels[4],
                       uint32_t *bm);
 
+/* The routed experts of one MoE layer over m rows, as QwenEngine encodes
+ * them per block (qwen.rs:2705-2735): moe_sort -> [moe_gather] -> grouped
+ * gate|up -> [swiglu_slots] -> grouped down (scatter to slot rows) ->
+ * moe_combine, on the stream, nothing allocated.  kernels: hb_engine_experts'
+ * four (sort, gate_up, down, gather or -1); swiglu: the swiglu_slots kernel
+ * (HB_KIND_SWIGLU, n = inter; ignored when the gate|up kernel is of kind
+ * HB_KIND_GEMM_SWIGLU); combine: moe_combine (n = hidden).  io as for
+ * hb_engine_experts (state[3] = m; route holds the m rows' route; xs is
+ * read only with a gather, egu only without the fused SwiGLU); out
+ * [m][hidden] bf16.  Every launch's bindings are checked first. */
+int hb_moe_experts_run(hb_gpu *gpu, const int32_t kernels[4], int32_t swiglu, int32_t combine,
+                       const hb_moe_io *io, hb_range out, uint32_t m);
+
 /* Seconds the engine spent timing candidates (autotune_seconds). */
 double hb_engine_autotune_seconds(hb_engine *engine);
 

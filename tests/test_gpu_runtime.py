@@ -28,16 +28,22 @@ def test_copy_and_refusals(gpu):
 
 
 def test_zero_ragged(gpu):
+    """hb_zero of byte ranges with a ragged head, a ragged tail, both inside
+    one 16-byte word, and whole words: exactly [offset, offset + bytes)
+    becomes zero."""
     a = np.full(1000, 0xAB, np.uint8)
     A = gpu.alloc_with(a)
     try:
-        gpu.zero(A, 3, 517)
-        got = gpu.download(A, np.uint8, 1000)
+        for off, n in [(3, 517), (0, 1000), (5, 3), (16, 32), (15, 2), (1, 15), (0, 1),
+                       (999, 1), (8, 992)]:
+            gpu.upload(A, a)
+            gpu.zero(A, off, n)
+            got = gpu.download(A, np.uint8, 1000)
+            want = a.copy()
+            want[off:off + n] = 0
+            assert np.array_equal(got, want), (off, n)
     finally:
         gpu.free(A)
-    want = a.copy()
-    want[3:520] = 0
-    assert np.array_equal(got, want)
 
 
 def test_native_cli_runs_gemm_and_matvec():
