@@ -76,6 +76,9 @@ struct hb_gpu {
     // than the 256 MiB last-level cache), built on first use.
     hb_buf flush_gu = 0, flush_h = 0;
     int32_t flush_kernel = -1;
+    // The device address of the library's static scratch on this device
+    // (hb_static.hip), taken at hb_open.
+    void* scratch = nullptr;
 };
 
 namespace hb {
@@ -87,6 +90,10 @@ int launch_ptrs(hb_gpu* g, int32_t kernel, void* const* ptrs, const uint64_t* si
                 uint32_t m);
 // The descriptor a kernel was built from (defaults filled), or null.
 const hb_desc* kernel_desc(hb_gpu* g, int32_t kernel);
+// The device address of the static scratch (hb_static.hip) on `device`,
+// which must be current: looked up, and its state word written, once per
+// device.
+int static_scratch(int device, void** out);
 // The routed experts of an MoE layer over device pointers (hb_moe.cpp):
 // bindings in hb_moe_io's order (state, route, list, tiles, x, w_gate_up,
 // egu, ehb, w_down, ey, xs), then out.

@@ -260,6 +260,13 @@ int hb_open(int device, hb_gpu** out) {
         delete g;
         return hip_fail(e, "stream/event");
     }
+    // The static scratch of hb_moe_experts_run_static on this device (the
+    // device is current): its address, once per device.
+    int rc = static_scratch(device, &g->scratch);
+    if (rc) {
+        hb_close(g);
+        return rc;
+    }
     *out = g;
     return HB_OK;
 }

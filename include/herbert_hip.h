@@ -331,6 +331,21 @@ int hb_engine_experts(hb_engine *engine, uint32_t experts, uint32_t top_k, uint3
 int hb_moe_experts_run(hb_gpu *gpu, const int32_t kernels[4], int32_t swiglu, int32_t combine,
                        const hb_moe_io *io, hb_range out, uint32_t m);
 
+/* hb_moe_experts_run with no caller workspace and nothing allocated: the
+ * sort's list and tile table, the gathered rows, the gate|up sums, the
+ * SwiGLU rows and the slot rows live in a fixed 64 MiB device array of
+ * the library (one per GPU, held until the process ends).  No counterpart
+ * in the reference; for callers that cannot allocate (code under HIP graph
+ * capture, tight decode loops, harnesses that forbid hipMalloc).  Rejects
+ * (HB_ERR_INVALID) a block whose intermediates exceed the array, e.g. more
+ * than ~700 rows at BASELINE config 5's shape (decode blocks of 1-64 rows
+ * need under 6 MiB).  Calls that overlap on one GPU share the array and
+ * race: issue them in stream order on one context per GPU.  Nothing in the
+ * array needs to start at zero (every intermediate a call reads, it wrote). */
+int hb_moe_experts_run_static(hb_gpu *gpu, const int32_t kernels[4], int32_t swiglu,
+                              int32_t combine, hb_range route, hb_range x, hb_range w_gate_up,
+                              hb_range w_down, hb_range out, uint32_t m);
+
 /* Seconds the engine spent timing candidates (autotune_seconds). */
 double hb_engine_autotune_seconds(hb_engine *engine);
 
