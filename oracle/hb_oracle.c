@@ -19,9 +19,17 @@
  *     an f64 restatement within one bf16 ulp;
  *   - hbo_moe_out: closed forms (zero gate weights: g = bf16(sigmoid(0)) =
  *     0.5; shared = 0: x + experts) and an f64 restatement;
- *   - hbo_route / hbo_moe_sort / hbo_combine / hbo_swiglu: brute-force
- *     restatements in numpy (argsort with ties, set invariants, tile cover),
- *     and hbo_expf against libm within 2 ulp over a dense sweep.
+ *   - hbo_route / hbo_moe_sort: brute-force restatements in numpy (argsort
+ *     with ties, set invariants, tile cover), and hbo_expf against libm
+ *     within 2 ulp over a dense sweep;
+ *   - hbo_swiglu: closed forms (g = 0 or u = 0: 0; g >= 20: sigmoid = 1 in
+ *     f32, h = bf16(g*u); g <= -104: 0) and one rounding of the f64 value
+ *     g*sigmoid(g)*u wherever that value is clear of a rounding boundary;
+ *   - hbo_combine: exact-term sums (f64), top_k 1 with weight 1 (identity),
+ *     and two hand-worked cases that fix the slot order, the rounding of
+ *     each partial sum and the rounding of each product;
+ *   and the swiglu / combine checks are shown to fail on builds of this
+ *   file with one deliberate error each (tests/test_oracle_mutants.py).
  *
  * Numerical contract: bf16 operands widened
  * exactly, products exact in f32, sums in f32 in increasing k order, one

@@ -19,7 +19,9 @@ import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, os.path.join(HERE, "..", "..", "oracle"))
+sys.path.insert(0, os.path.join(HERE, ".."))
 import hb_oracle as orc  # noqa: E402
+from test_oracle import combine_pins, swiglu_pins  # noqa: E402
 
 
 def f32(b):
@@ -100,17 +102,37 @@ def main():
     assert sorted(lst) == list(range(72))
     g["list"], g["tiles"] = lst, tiles[:1 + 3 * int(tiles[0])]
 
-    # a12: SwiGLU; a5: fused [gate | up] GEMM + SwiGLU on exact sums
+    # a12: SwiGLU (the oracle first passes the pins the mathematics fixes);
+    # the fixture within 1 ulp of f64, and one rounding of the f64 value
+    # wherever that value is clear of a rounding boundary.
+    swiglu_pins(orc.swiglu)
+    combine_pins(orc.combine)
     gu = rne_branchy((2 * rng.standard_normal((3, 64))).astype(np.float32).view(np.uint32))
     g["gu"], g["h"] = gu, orc.swiglu(gu, 32)
+    gf, uf = f32(gu[:, :32]).astype(np.float64), f32(gu[:, 32:]).astype(np.float64)
+    t = gf / (1 + np.exp(-gf)) * uf
+    ulp = np.exp2(np.floor(np.log2(np.maximum(np.abs(t), 2.0 ** -126))) - 7)
+    assert np.all(np.abs(f32(g["h"]) - t) <= ulp)
+    frac = np.abs(t) / ulp - np.floor(np.abs(t) / ulp)
+    clear = np.abs(frac - 0.5) > 2.0 ** -12
+    assert np.array_equal(g["h"][clear], rne_branchy(t.astype(np.float32).view(np.uint32))[clear])
+    # a5: fused [gate | up] GEMM + SwiGLU on exact sums
     xs = exact_bf16(rng, (4, 64))
     ws = exact_bf16(rng, (48, 64), -4, 0)
     g["sx"], g["sw"], g["sh"] = xs, ws, orc.gemm_swiglu(xs, ws, 24)
     assert np.array_equal(g["sh"], orc.swiglu(orc.gemm(xs, ws, orc.OUT_BF16), 24))
 
-    # a13: combine of the routed slots
+    # a13: combine of the routed slots, each step from exact f64 values (a
+    # bf16 product and a sum of two bf16 are exact in f64) rounded by the
+    # branchy RNE, in the route's slot order.
     y = rne_branchy(rng.standard_normal((9 * 8, 32)).astype(np.float32).view(np.uint32))
     g["cy"], g["cout"] = y, orc.combine(y, route, 8, 32)
+    rb64 = lambda v: f32(rne_branchy(np.asarray(v, np.float64).astype(np.float32).view(np.uint32)))  # noqa: E731
+    wts = route[:, 8:].view(np.float32).astype(np.float64)
+    acc = np.zeros((9, 32))
+    for s_ in range(8):
+        acc = rb64(acc + rb64(f32(y).reshape(9, 8, 32)[:, s_].astype(np.float64) * wts[:, s_:s_ + 1]))
+    assert np.array_equal(f32(g["cout"]), acc)
 
     # expf samples (the route's softmax and SwiGLU's sigmoid)
     xe = np.concatenate([np.linspace(-100, 88, 97), [-104.0, 89.0, 0.0, -0.0, 1e-30, -1e-30]]).astype(np.float32)

@@ -269,36 +269,126 @@ def test_experts_gemm_equals_dense_gemm_per_expert():
         assert np.array_equal(y[pair], want[0])
 
 
-def test_swiglu_and_fused_swiglu():
+# ---- swiglu_slots / moe_combine: checks the mathematics fixes ------------
+# (qwen_kernels.rs:2087-2117: h = bf16(g * sigmoid(g) * u) in f32, one
+# rounding; qwen_kernels.rs:2119-2165: acc = bf16(acc + bf16(y_s * w_s)) over
+# the slots in route order.)  Written as functions of the implementation so
+# that tests/test_oracle_mutants.py can run them against deliberately wrong
+# builds of the oracle and see them fail.
+
+
+def _bf16_of(v):
+    """RNE of f32 values to bf16 bits (the reference's branchy form)."""
+    return rne_branchy(np.asarray(v, np.float32).view(np.uint32))
+
+
+def _ulp(v):
+    a = np.abs(np.asarray(v, np.float64))
+    return np.exp2(np.floor(np.log2(np.maximum(a, 2.0 ** -126))) - 7)
+
+
+def swiglu_pins(swiglu):
+    """swiglu(gu [slots][2n] bf16 bits, n) -> h [slots][n] bf16 bits."""
+    rng = np.random.default_rng(0x5A1)
+    n = 512
+    u = _bf16_of(rng.standard_normal(n) * 2)
+    g = _bf16_of(rng.standard_normal(n) * 2)
+    # g = 0 or u = 0: h is zero (of either sign).
+    zero = np.zeros(n, np.uint16)
+    for gg, uu in ((zero, u), (g, zero)):
+        h = swiglu(np.concatenate([gg, uu])[None], n)[0]
+        assert np.all(bf16_to_f32(h) == 0), "swiglu with a zero factor"
+    # g >= 20: sigmoid(g) is 1 in f32 (1 - 2e-9), so h = bf16(g * u), the
+    # product of two bf16 exact in f32.
+    big = _bf16_of(20 + np.abs(rng.standard_normal(n)) * 30)
+    h = swiglu(np.concatenate([big, u])[None], n)[0]
+    assert np.array_equal(h, _bf16_of(bf16_to_f32(big) * bf16_to_f32(u))), "swiglu at g >= 20"
+    # g <= -104: exp(-g) overflows f32, sigmoid is 0, h = 0.
+    neg = _bf16_of(-104 - np.abs(rng.standard_normal(n)) * 50)
+    h = swiglu(np.concatenate([neg, u])[None], n)[0]
+    assert np.all(bf16_to_f32(h) == 0), "swiglu at g <= -104"
+    # Random g in [-12, 12]: h is the f64 value g * sigmoid(g) * u rounded
+    # once to bf16, wherever that value sits further than 2^-12 of an ulp
+    # from a rounding boundary (the f32 evaluation's error is ~2^-22
+    # relative): a rounding of g * sigmoid(g) before the multiply by u, or a
+    # wrong sigmoid, moves many outputs by an ulp.  Everywhere within 1 ulp.
+    slots = 64
+    gg = _bf16_of(rng.uniform(-12, 12, (slots, n)))
+    uu = _bf16_of(rng.standard_normal((slots, n)) * 3)
+    h = swiglu(np.concatenate([gg, uu], axis=1), n)
+    gf, uf = bf16_to_f32(gg).astype(np.float64), bf16_to_f32(uu).astype(np.float64)
+    t = gf / (1.0 + np.exp(-gf)) * uf
+    hf = bf16_to_f32(h).astype(np.float64)
+    assert np.all(np.abs(hf - t) <= _ulp(t)), "swiglu beyond 1 ulp of f64"
+    frac = np.abs(t) / _ulp(t)
+    frac -= np.floor(frac)
+    clear = (np.abs(frac - 0.5) > 2.0 ** -12) & (np.abs(t) > 2.0 ** -100)
+    assert clear.mean() > 0.95
+    want = _bf16_of(t.astype(np.float32))
+    bad = (h != want) & clear
+    assert not bad.any(), "swiglu != one rounding of g*sigmoid(g)*u at %d outputs" % bad.sum()
+
+
+def _route(experts_rows, weights):
+    weights = np.asarray(weights, np.float32)
+    rows, k = weights.shape
+    r = np.zeros((rows, 2 * k), np.uint32)
+    r[:, :k] = experts_rows
+    r[:, k:] = weights.view(np.uint32)
+    return r
+
+
+def combine_pins(combine):
+    """combine(y [rows*k][d] bf16 bits, route [rows][2k], k, d) -> [rows][d]."""
+    rng = np.random.default_rng(0xC0B)
+    rows, k, d = 16, 8, 64
+    ex = np.sort(rng.choice(256, (rows, k)), axis=1)
+    # Every rounding exact: small integers times 1/2 or 1/4, partial sums
+    # below 2^5 in steps of 1/4 (8 significant bits suffice): the f64 sum.
+    y = rng.integers(-3, 4, (rows * k, d)).astype(np.float32)
+    w = rng.choice([0.25, 0.5], (rows, k)).astype(np.float32)
+    out = combine(_bf16_of(y), _route(ex, w), k, d)
+    want = (y.reshape(rows, k, d).astype(np.float64) * w[:, :, None]).sum(axis=1)
+    assert np.array_equal(bf16_to_f32(out).astype(np.float64), want), "combine of exact terms"
+    # One slot of weight 1: the identity.
+    y1 = _bf16_of(rng.standard_normal((rows, d)))
+    out = combine(y1, _route(ex[:, :1], np.ones((rows, 1), np.float32)), 1, d)
+    assert np.array_equal(out, y1), "combine with top_k 1, weight 1"
+    # Planted: slots (256, 1, -256), weights 1, in slot order with each sum
+    # rounded: 256 + 1 = 257 ties to 256 (bf16 spacing 2 there), 256 - 256 =
+    # 0.  Reversed order gives -256 + 1 = -255 (exact), then + 256 = 1; one
+    # rounding at the end gives 1.
+    yp = np.zeros((1, 3, d), np.float32)
+    yp[0, :, 0] = [256.0, 1.0, -256.0]
+    out = combine(_bf16_of(yp.reshape(3, d)), _route([[3, 7, 9]], [[1.0, 1.0, 1.0]]), 3, d)
+    assert bf16_to_f32(out)[0, 0] == 0.0, "combine order / per-step rounding"
+    # Planted: the product rounded before the add.  Slot 0: 1 * 1 = 1.
+    # Slot 1: y = (1 + 66/128)/16, w = (1 + 125/128)/16, y*w =
+    # 0.011702060699462890625 rounds to 3 * 2^-8 = 0.01171875; 1 + that =
+    # 1 + 1.5 * 2^-7 is a tie that goes to the even 1 + 2^-6 = 1.015625.
+    # Unrounded, 1 + 0.0117020607 is below the tie: 1 + 2^-7.
+    yq = np.zeros((2, d), np.float32)
+    yq[:, 0] = [1.0, (1 + 66 / 128) / 16]
+    out = combine(_bf16_of(yq), _route([[1, 2]], [[1.0, (1 + 125 / 128) / 16]]), 2, d)
+    assert bf16_to_f32(out)[0, 0] == 1.015625, "combine product rounding"
+
+
+def test_swiglu_pinned():
+    swiglu_pins(lambda gu, n: orc.swiglu(gu, n))
+
+
+def test_combine_pinned():
+    combine_pins(lambda y, route, k, d: orc.combine(y, route, k, d))
+
+
+def test_fused_swiglu_is_gemm_then_swiglu():
+    """prefill.rs:746-750: the fused [gate | up] GEMM + SwiGLU is bit-equal to
+    the GEMM (Out::Bf16) followed by swiglu_rows."""
     rng = np.random.default_rng(8)
     n = 48
-    gu = orc_f32_to_bf16(rng.standard_normal((10, 2 * n)) * 3)
-    h = orc.swiglu(gu, n)
-    g = bf16_to_f32(gu[:, :n])
-    u = bf16_to_f32(gu[:, n:])
-    sig = (np.float32(1) / (np.float32(1) + np_expf(-g))).astype(np.float32)
-    want = orc_f32_to_bf16(((g * sig).astype(np.float32) * u).astype(np.float32))
-    assert np.array_equal(h, want)
     x = orc_f32_to_bf16(rng.standard_normal((6, 64)))
     w = orc_f32_to_bf16(rng.standard_normal((2 * n, 64)) * 0.1)
     assert np.array_equal(orc.gemm_swiglu(x, w, n), orc.swiglu(orc.gemm(x, w), n))
-
-
-def test_combine_order_and_rounding():
-    rng = np.random.default_rng(9)
-    rows, top_k, d = 7, 8, 40
-    route = np.zeros((rows, 2 * top_k), np.uint32)
-    wts = orc_f32_to_bf16(rng.random((rows, top_k)).astype(np.float32) / 4)
-    route[:, top_k:] = wts.astype(np.uint32) << np.uint32(16)
-    y = orc_f32_to_bf16(rng.standard_normal((rows * top_k, d)))
-    got = orc.combine(y, route, top_k, d)
-    yf = bf16_to_f32(y).reshape(rows, top_k, d)
-    wf = bf16_to_f32(wts)
-    acc = np.zeros((rows, d), np.float32)
-    for s in range(top_k):
-        c = bf16_to_f32(orc_f32_to_bf16((yf[:, s] * wf[:, s:s + 1]).astype(np.float32)))
-        acc = bf16_to_f32(orc_f32_to_bf16((acc + c).astype(np.float32)))
-    assert np.array_equal(got, orc_f32_to_bf16(acc))
 
 
 # ---- decode fusion XSrc::Norm (kernels.rs:48-103, 355-440) ---------------
