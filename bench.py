@@ -67,25 +67,115 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
+def _median3(fn):
+    ts = []
+    for _ in range(3):
+        t = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t)
+    return sorted(ts)[1]
+
+
 def cpu_baseline(rows):
-    """The contract's scalar f32 GEMM (oracle/hb_oracle.c) on the host's
-    cores over `rows` rows of each of the step's four GEMMs."""
+    """The contract's scalar CPU restatement (oracle/hb_oracle.c: f32 sums
+    in increasing k, one rounding) on the host's cores, each figure the
+    median of 3 runs: the metric's GEMMs over `rows` rows of each of the
+    step's four (the headline `value`), and beside it config 1 whole, the
+    decode step at M=1 (four layers + lm_head) and the MoE layer's grouped
+    GEMMs over a sample of tokens."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import hb_oracle as orc
     import herbert_hip as hb
-    threads = min(16, os.cpu_count() or 1)
+    host = os.cpu_count() or 1
+    # The GPU box gives one GPU's job a share of 16 host CPUs, whatever
+    # os.cpu_count() reports there; this build's container has 8.
+    threads = min(16, host)
     flops, secs = 0.0, 0.0
     for i, (name, k, n, out) in enumerate(LAYER):
         x = hb.normal_bf16(SEED + 2 * i, 1.0, (rows, k))
         w = hb.normal_bf16(SEED + 2 * i + 1, 0.02, (n, k))
         y0 = hb.normal_bf16(SEED + 100 + i, 1.0, (rows, n)) if out == 2 else None
-        t = time.perf_counter()
-        orc.gemm(x, w, out, y0, threads=threads)
-        secs += time.perf_counter() - t
+        secs += _median3(lambda: orc.gemm(x, w, out, y0, threads=threads))
         flops += 2.0 * rows * n * k
-    return {"value": flops / secs / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-            "sample": "%d of the %d rows of each of the 4 GEMMs (oracle/hb_oracle.c, scalar f32 "
-                      "in k order, %d threads), %.1f s" % (rows, M, threads, secs)}
+    res = {"value": flops / secs / 1e12, "unit": "TFLOP/s", "cores": threads, "host_cpus": host,
+           "kind": "port", "median_of": 3,
+           "sample": "%d of the %d rows of each of the 4 GEMMs (oracle/hb_oracle.c, scalar f32 in k "
+                     "order, %d threads: the box's CPU share for one GPU), %.1f s per run" % (
+                         rows, M, threads, secs)}
+    # config 1, whole
+    k, n = CONFIG1[0][1], CONFIG1[0][2]
+    x = hb.normal_bf16(0x5EED0001, 1.0, (512, k))
+    w = hb.normal_bf16(0x5EED0002, 0.02, (n, k))
+    t = _median3(lambda: orc.gemm(x, w, 0, threads=threads))
+    res["config1"] = {"value": round(2.0 * 512 * n * k / t / 1e12, 4), "unit": "TFLOP/s", "s": round(t, 3)}
+    # decode M=1: the step's weights (4 layers + lm_head) streamed once
+    nbytes, t = 0.0, 0.0
+    for name, k, n, o in LAYER + [LM_HEAD]:
+        layers = 1 if name == "lm_head" else DECODE_LAYERS
+        w = hb.normal_bf16(0x5EED0003 + n, 0.02, (n, k))
+        x = hb.normal_bf16(0x5EED0003, 1.0, (1, k))
+        y0 = hb.normal_bf16(5, 1.0, (1, n)) if o == 2 else None
+        t += layers * _median3(lambda: orc.gemm(x, w, o, y0, threads=threads))
+        nbytes += layers * (2.0 * n * k + 2.0 * k + 2.0 * n * (2 if o == 2 else 1))
+    res["decode_m1"] = {"value": round(nbytes / t / 1e9, 2), "unit": "GB/s", "s": round(t, 3)}
+    # MoE (config 5): the grouped gate|up and down over 256 of the 2048
+    # tokens (their route from the seeded logits), all 256 experts' weights
+    T5, E, TOPK, H, MI = 256, 256, 8, 2048, 512
+    scores = hb.normal_bf16(0x5EED0005, 1.0, (T5, E))
+    route = orc.route(scores, TOPK)
+    lst, tiles = orc.moe_sort(route, TOPK, E, 64)
+    wgu = hb.normal_bf16(0x5EED0006, 0.02, (E * 2 * MI, H))
+    wdn = hb.normal_bf16(0x5EED0007, 0.02, (E * H, MI))
+    xx = hb.normal_bf16(0x5EED0008, 1.0, (T5, H))
+    P = T5 * TOPK
+    hh = hb.normal_bf16(0x5EED0009, 1.0, (P, MI))
+    t = _median3(lambda: (orc.experts_gemm(xx, wgu, lst, tiles, H, 2 * MI, 1, TOPK, P, threads=threads),
+                          orc.experts_gemm(hh, wdn, lst, tiles, MI, H, 2, TOPK, P, threads=threads)))
+    res["moe"] = {"value": round(2.0 * P * 3 * MI * H / t / 1e12, 4), "unit": "TFLOP/s", "s": round(t, 3),
+                  "sample": "%d tokens x top %d, the grouped gate|up and down" % (T5, TOPK)}
+    return res
+
+
+def yardstick(steps):
+    """hipBLASLt through torch.matmul (bf16, the same shapes and seeds) as a
+    yardstick for the prefill GEMMs: each shape alone, warm, and the four
+    of the step back to back.  Printed as text (profiles/); torch is used
+    here only, never by the library."""
+    import torch
+    import herbert_hip as hb
+    dev = torch.device("cuda:0")
+
+    def t_of(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / 1e3 / reps
+
+    lines = ["hipBLASLt (torch %s, torch.matmul bf16 -> bf16) on %s" % (torch.__version__,
+                                                                         torch.cuda.get_device_name(0))]
+    mats = []
+    for i, (name, k, n, out) in enumerate(LAYER):
+        x = torch.from_numpy(hb.normal_bf16(SEED + 2 * i, 1.0, (M, k)).view(np.int16)).view(torch.bfloat16).to(dev)
+        w = torch.from_numpy(hb.normal_bf16(SEED + 2 * i + 1, 0.02, (n, k)).view(np.int16)).view(torch.bfloat16).to(dev)
+        mats.append((name, k, n, x, w))
+        t = t_of(lambda: torch.matmul(x, w.t()), steps)
+        lines.append("  %-8s M=%d K=%d N=%d alone: %8.2f us %7.1f TFLOP/s" % (name, M, k, n, t * 1e6,
+                                                                             2.0 * M * n * k / t / 1e12))
+    step = lambda: [torch.matmul(x, w.t()) for _, _, _, x, w in mats]  # noqa: E731
+    t = t_of(step, steps)
+    fl = sum(2.0 * M * n * k for _, k, n, _, _ in mats)
+    lines.append("  step (qkv, o, gate_up, down back to back): %8.2f us %7.1f TFLOP/s" % (t * 1e6, fl / t / 1e12))
+    s = 8192
+    a = torch.randn(s, s, device=dev, dtype=torch.bfloat16)
+    bmat = torch.randn(s, s, device=dev, dtype=torch.bfloat16)
+    t = t_of(lambda: torch.matmul(a, bmat.t()), 10)
+    lines.append("  8192^3: %8.2f us %7.1f TFLOP/s" % (t * 1e6, 2.0 * s ** 3 / t / 1e12))
+    print("\n".join(lines), flush=True)
 
 
 def main():
@@ -94,7 +184,7 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--tune", default="")
-    ap.add_argument("--cpu-rows", type=int, default=1536)
+    ap.add_argument("--cpu-rows", type=int, default=512)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-matvec", action="store_true")
     ap.add_argument("--no-moe", action="store_true")
@@ -102,12 +192,17 @@ def main():
     ap.add_argument("--traffic-run", action="store_true")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     ap.add_argument("--trace-summary", nargs=3, metavar=("TRACE_CSV", "BENCH_OUT", "COMMAND"))
+    ap.add_argument("--yardstick", action="store_true",
+                    help="time hipBLASLt (torch.matmul) on the step's shapes instead")
     args = ap.parse_args()
     if args.traffic_summary:
         traffic_summary(*args.traffic_summary)
         return
     if args.trace_summary:
         trace_summary(*args.trace_summary)
+        return
+    if args.yardstick:
+        yardstick(args.steps)
         return
     if args.gpus != 1:
         print("bench.py: this build runs on one GPU only (--gpus %d asked); the path would shard "
@@ -413,6 +508,25 @@ def bench_moe(g, e, hb):
     out["value"] = round((gu_b + dn_b) / (per["gate_up"] + per["down"]) / 1e9, 1)
     out["frac"] = round(out["value"] / HBM_PEAK, 4)
     layer.free()
+    # The tile rows the config names (16, 32, 64; moe.tile, qwen.rs:161-164
+    # publishes the reference's layer rate per tile size): the layer on
+    # each, the rest of its selection timed as above.
+    out["tiles"] = {}
+    for bm in (16, 32, 64):
+        with hb.Engine(g, "moe.tile=%d" % bm) as et:
+            lt = hb.MoeLayer(g, et, E, TOPK, H, MI, T, wgu, wdn, scores=hb.normal_bf16(seed, 1.0, (T, E)),
+                             x=hb.normal_bf16(seed + 3, 1.0, (T, H)))
+        lops = lt.ops()
+        g.time_ops(lops, 3)
+        tt, ee = g.time_each(lops, reps)
+        nm_t = ["route", "sort"] + (["gather"] if lt.kernels[3] >= 0 else []) + \
+            ["gate_up"] + ([] if lt.fused else ["swiglu"]) + ["down", "combine"]
+        pt = dict(zip(nm_t, ee))
+        out["tiles"][str(bm)] = {"layer_us": round(tt / reps * 1e6, 2), "gate_up_us": round(pt["gate_up"] * 1e6, 2),
+                                 "down_us": round(pt["down"] * 1e6, 2),
+                                 "gate_up_kernel": g.kernel_name(lt.kernels[1]),
+                                 "down_kernel": g.kernel_name(lt.kernels[2])}
+        lt.free()
     # The whole sparse MLP (qwen.rs:2691-2732): post norm, shared expert
     # (inter 512), router GEMM, the routed experts above, moe_out.
     SI = 512
