@@ -601,6 +601,19 @@ const char* hb_engine_log(hb_engine* e) { return e->log.c_str(); }
 
 double hb_engine_autotune_seconds(hb_engine* e) { return e->autotune_seconds; }
 
+int hb_engine_tune_get(hb_engine* e, const char* key, uint32_t* value) {
+    auto it = e->t.v.find(key ? key : "");
+    if (it == e->t.v.end()) return fail(HB_ERR_INVALID, std::string("--tune: unknown key ") + (key ? key : ""));
+    *value = it->second;
+    return HB_OK;
+}
+
+int hb_engine_log_line(hb_engine* e, const char* line, double seconds) {
+    e->logf("%s", line ? line : "");
+    e->autotune_seconds += seconds;
+    return HB_OK;
+}
+
 int hb_tune_check(const char* tune, char* summary, uint64_t cap) {
     Tune t;
     std::string err;

@@ -202,6 +202,8 @@ lib.hb_engine_gemm_candidates.argtypes = [_P, _u32, _u32, _u32, ctypes.POINTER(D
                                           ctypes.POINTER(_u32)]
 lib.hb_moe_experts_run.argtypes = [_P, ctypes.POINTER(_i32), _i32, _i32, ctypes.POINTER(MoeIo), Range,
                                    _u32]
+lib.hb_engine_tune_get.argtypes = [_P, ctypes.c_char_p, ctypes.POINTER(_u32)]
+lib.hb_engine_log_line.argtypes = [_P, ctypes.c_char_p, ctypes.c_double]
 lib.hb_engine_autotune_seconds.argtypes = [_P]
 lib.hb_engine_autotune_seconds.restype = ctypes.c_double
 
@@ -462,6 +464,16 @@ class Engine:
 
     def add_gemm_candidate(self, name, desc):
         check(lib.hb_engine_add_gemm_candidate(self.h, name.encode(), ctypes.byref(desc)))
+
+    def tune_get(self, key):
+        """The --tune value of `key` (defaults + the engine's string)."""
+        v = _u32()
+        check(lib.hb_engine_tune_get(self.h, key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def log_line(self, line, seconds=0.0):
+        """A line of the host's own timed choice into the engine's log."""
+        check(lib.hb_engine_log_line(self.h, line.encode(), float(seconds)))
 
     def gemm_candidates(self, k, n, out):
         """The descriptors gemm() times for a k x n GEMM, in candidate order."""
@@ -785,13 +797,13 @@ class PrefillMlp:
             self.kern[m] = (gu_k, sw_k, dn_k)
             g.free(st)
 
-    def ops(self, x, n, states):
+    def ops(self, x, n, states, chunk=None):
         """The ops of a prompt of n rows of the residual stream `x` (a buffer
         of [n][hidden] bf16, updated in place); `states`: one state buffer per
         block (blocks_of(n, chunk)), state[3] its rows."""
         h, b, w = self.h, self.buf, self.w
         ops = []
-        for (start, rows), st in zip(blocks_of(n, self.chunk), states):
+        for (start, rows), st in zip(blocks_of(n, chunk or self.chunk), states):
             m = min(bk for bk in self.buckets if bk >= rows)
             gu_k, sw_k, dn_k = self.kern[m]
             xr = r(x, start * h * 2, rows * h * 2)
@@ -805,11 +817,143 @@ class PrefillMlp:
             ops.append(Op(dn_k, [s, r(w["down"]), r(b["hh"]), xr, s, s], rows))
         return ops
 
-    def states(self, n):
+    def states(self, n, chunk=None):
         """One state buffer per block of a prompt of n rows (free them after)."""
         return [self.gpu.alloc_with(np.array([0, 0, 0, rows], np.uint32))
-                for _, rows in blocks_of(n, self.chunk)]
+                for _, rows in blocks_of(n, chunk or self.chunk)]
+
+    def autotune_chunk(self, engine, seed=0x5EED00C0):
+        """autotune_chunk (qwen.rs:2962-3027) over this MLP half: a prompt of
+        prefill.block rows (seeded N(0,1) residual rows, the reference's
+        probe ids) cut by each of 1024, 2048, 4096, 8192 rows below
+        prefill.block and by prefill.block itself (blocks_of), the first
+        candidate run until auto.heat ms of GPU time have passed, then three
+        rounds in alternating order, the median of each; the fastest kept
+        as self.chunk and logged as the reference logs it."""
+        import time
+        t0 = time.time()
+        block = engine.tune_get("prefill.block")
+        cands = [c for c in (1024, 2048, 4096, 8192) if c < block] + [block]
+        if len(cands) < 2:
+            return self.chunk
+        g, n = self.gpu, block
+        x0 = normal_bf16(seed, 1.0, (n, self.h))
+        X = g.alloc_with(x0)
+        plans = {}
+        try:
+            for c in cands:
+                st = self.states(n, c)
+                plans[c] = (st, self.ops(X, n, st, c))
+
+            def run(c):
+                g.upload(X, x0)  # reset: the block adds into x
+                return g.time_ops(plans[c][1], 1)
+
+            heat = engine.tune_get("auto.heat") * 1e-3
+            warmed = run(cands[0])
+            while warmed < heat:
+                warmed += run(cands[0])
+            times = {c: [] for c in cands}
+            for rnd in range(3):
+                for c in (cands if rnd % 2 == 0 else cands[::-1]):
+                    times[c].append(run(c))
+            med = {c: sorted(v)[1] for c, v in times.items()}
+            best = min(cands, key=lambda c: med[c])
+            self.chunk = best
+            engine.log_line("[autotune] blocks over %d rows, every layer, heated %.1f s, median of 3 rounds: %s -> %d"
+                            % (block, warmed, ", ".join("%d %.3f ms" % (c, med[c] * 1e3) for c in cands), best),
+                            time.time() - t0)
+            return best
+        finally:
+            for st, _ in plans.values():
+                for b in st:
+                    g.free(b)
+            g.free(X)
 
     def free(self):
         for buf in list(self.buf.values()) + list(self.w.values()):
             self.gpu.free(buf)
+
+
+class PrefillAttnProj:
+    """The projections of an attention layer's prefill (block_in, qwen.rs:
+    2653-2668): x -> input norm -> the fused [q | k | v] GEMM (Bf16 into
+    `qkv`, [n][q_width + 2 kv_width]); and o from the attention's output
+    added to x (Out::Residual).  RoPE and the attention itself sit between
+    them in the reference and are not part of this library: the caller
+    brings the attention output.  Weights from the checkpoint, [q | k | v]
+    stacked as QwenEngine::load does (qwen.rs:831-835); blocks and buckets
+    as PrefillMlp."""
+
+    def __init__(self, gpu, engine, ckpt, layer, hidden, q_width, kv_width, out_width, eps=1e-6,
+                 plus_one=True):
+        self.gpu, self.h, self.qkv_w, self.out_w = gpu, hidden, q_width + 2 * kv_width, out_width
+        p = lambda f: "%d.%s" % (layer, f)  # noqa: E731
+        self.w = {"input_norm": ckpt.upload(gpu, [(p("input_layernorm.weight"), hidden)]),
+                  "qkv": ckpt.upload(gpu, [(p("self_attn.q_proj.weight"), q_width * hidden),
+                                           (p("self_attn.k_proj.weight"), kv_width * hidden),
+                                           (p("self_attn.v_proj.weight"), kv_width * hidden)]),
+                  "o": ckpt.upload(gpu, [(p("self_attn.o_proj.weight"), hidden * out_width)])}
+        self.buckets = engine.buckets()
+        self.chunk = self.buckets[-1]
+        B = self.chunk
+        g = gpu
+        self.buf = {"xn": g.alloc(B * hidden * 2)}
+        self.norm_k = g.pipeline(rmsnorm(hidden, eps, plus_one))
+        self.kern = {}
+        for m in self.buckets:
+            st = g.alloc_with(np.array([0, 0, 0, m], np.uint32))
+            qkv_t, ao_t, x_t = g.alloc(m * self.qkv_w * 2), g.alloc(m * out_width * 2), g.alloc(m * hidden * 2)
+            qk = engine.gemm(hidden, self.qkv_w, Out.Bf16, r(st), r(self.w["qkv"]), r(self.buf["xn"]), r(qkv_t), m)
+            ok = engine.gemm(out_width, hidden, Out.Residual, r(st), r(self.w["o"]), r(ao_t), r(x_t), m)
+            self.kern[m] = (qk, ok)
+            for b in (st, qkv_t, ao_t, x_t):
+                g.free(b)
+
+    def ops_qkv(self, x, qkv, n, states):
+        """norm + [q | k | v] of a prompt of n rows: x [n][hidden] -> qkv."""
+        ops = []
+        for (start, rows), st in zip(blocks_of(n, self.chunk), states):
+            qk, _ = self.kern[min(bk for bk in self.buckets if bk >= rows)]
+            s = r(st)
+            ops.append(Op(self.norm_k, [r(x, start * self.h * 2, rows * self.h * 2), r(self.w["input_norm"]),
+                                        r(self.buf["xn"])], rows))
+            ops.append(Op(qk, [s, r(self.w["qkv"]), r(self.buf["xn"]),
+                               r(qkv, start * self.qkv_w * 2, rows * self.qkv_w * 2), s, s], rows))
+        return ops
+
+    def ops_o(self, attn_out, x, n, states):
+        """x += o(attn_out) over a prompt of n rows."""
+        ops = []
+        for (start, rows), st in zip(blocks_of(n, self.chunk), states):
+            _, ok = self.kern[min(bk for bk in self.buckets if bk >= rows)]
+            s = r(st)
+            ops.append(Op(ok, [s, r(self.w["o"]), r(attn_out, start * self.out_w * 2, rows * self.out_w * 2),
+                               r(x, start * self.h * 2, rows * self.h * 2), s, s], rows))
+        return ops
+
+    def states(self, n):
+        return [self.gpu.alloc_with(np.array([0, 0, 0, rows], np.uint32)) for _, rows in blocks_of(n, self.chunk)]
+
+    def free(self):
+        for buf in list(self.buf.values()) + list(self.w.values()):
+            self.gpu.free(buf)
+
+
+def moe_weights_from_checkpoint(gpu, ckpt, layer, experts, hidden, inter, shared_inter):
+    """The device weights of a qwen3_5_moe layer's sparse MLP as
+    QwenEngine::load uploads them (qwen.rs:788-801): the post norm, the
+    router (mlp.gate), the experts' [gate | up] rows and down rows
+    (mlp.experts.gate_up_proj [E][2 inter][h], down_proj [E][h][inter]),
+    the shared expert stacked [gate | up], its down and its gate; the dict
+    MoeBlock takes."""
+    p = lambda f: "%d.%s" % (layer, f)  # noqa: E731
+    h, e, mi, si = hidden, experts, inter, shared_inter
+    return {"post_norm": ckpt.upload(gpu, [(p("post_attention_layernorm.weight"), h)]),
+            "router": ckpt.upload(gpu, [(p("mlp.gate.weight"), e * h)]),
+            "w_gate_up": ckpt.upload(gpu, [(p("mlp.experts.gate_up_proj"), e * 2 * mi * h)]),
+            "w_down": ckpt.upload(gpu, [(p("mlp.experts.down_proj"), e * h * mi)]),
+            "s_gate_up": ckpt.upload(gpu, [(p("mlp.shared_expert.gate_proj.weight"), si * h),
+                                           (p("mlp.shared_expert.up_proj.weight"), si * h)]),
+            "s_down": ckpt.upload(gpu, [(p("mlp.shared_expert.down_proj.weight"), h * si)]),
+            "shared_gate": ckpt.upload(gpu, [(p("mlp.shared_expert_gate.weight"), h)])}

@@ -348,6 +348,15 @@ int hb_moe_experts_run_static(hb_gpu *gpu, const int32_t kernels[4], int32_t swi
 
 /* Seconds the engine spent timing candidates (autotune_seconds). */
 double hb_engine_autotune_seconds(hb_engine *engine);
+/* The value of a --tune key after defaults and hb_engine_open's string (the
+ * fields QwenEngine reads from self.tune, e.g. prefill.block, auto.heat);
+ * HB_ERR_INVALID for a key the table does not hold. */
+int hb_engine_tune_get(hb_engine *engine, const char *key, uint32_t *value);
+/* A line of the host's own timed choices (the reference's eprintln! of
+ * QwenEngine, e.g. autotune_chunk's "[autotune] blocks over ..." at
+ * qwen.rs:3003) into the engine's log and stderr; `seconds` of timing are
+ * added to hb_engine_autotune_seconds. */
+int hb_engine_log_line(hb_engine *engine, const char *line, double seconds);
 
 /* Every line the engine logged ([autotune] ..., [hip] ...), also written to
  * stderr as the reference's eprintln! does. */
