@@ -38,6 +38,7 @@ static bool is_gemm(uint32_t kind) {
 
 hb_desc with_defaults(const hb_desc& in) {
     hb_desc d = in;
+    if (d.ksplit == 1) d.ksplit = 0;  // one part: no split
     if (d.kind == HB_KIND_GEMM || d.kind == HB_KIND_GEMM_SWIGLU) {
         bool experts = d.rows_of != HB_ROWS_DENSE;
         if (!d.bm) d.bm = experts ? 32 : 128;
@@ -134,8 +135,14 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
             if (d.sched &&
                 (uint64_t)(d.dbuf + 1) * (d.bm + d.bn) * d.bk * 2 > 160 * 1024)
                 return fail(HB_ERR_UNSUPPORTED, "gemm (pipelined schedules): stages beyond 160 KiB of LDS");
+            if (d.ksplit > 16 || (d.ksplit > 1 && (swi || experts || d.k % (d.bk * d.ksplit) ||
+                                                   (d.sched == 3 && (d.k / d.bk / d.ksplit) % 2))))
+                return fail(HB_ERR_UNSUPPORTED,
+                            "gemm split K: 2..16 parts, dense rows, K a multiple of bk x parts "
+                            "(sched 3: an even count of K tiles per part)");
             std::string band = d.band ? "_b" + std::to_string(d.band) : "";
             if (d.w_nt) band += "_wnt";
+            if (d.ksplit > 1) band += "_ks" + std::to_string(d.ksplit);
             if (d.sched) band += d.sched == 1 ? "_pp" : d.sched == 2 ? "_pp2" : "_il";
             snprintf(name, sizeof name, "gemm_mma%s_%ux%u_%s%s_t%ux%u_k%u_w%ux%u_x%u_d%u%s_s%u_o%u%s%s",
                      swi ? "_swiglu" : "", d.k, d.n, out_tag(d.out), d.m_first ? "_mf" : "", d.bn,
@@ -153,12 +160,28 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
                           D("HB_ORDER", d.order), D("HB_MFIRST", d.m_first ? 1 : 0),
                           D("HB_DMA", d.lds_dma ? 1 : 0), D("HB_SWIGLU", swi ? 1 : 0),
                           D("HB_BAND", d.band), D("HB_W_NT", d.w_nt)};
+            if (d.ksplit > 1) {
+                // The parts' f32 sums into the workspace; Out is the second
+                // kernel's.
+                e->defines[2] = D("HB_OUT", HB_OUT_F32);
+                e->defines.push_back(D("HB_KSPLIT", d.ksplit));
+            }
             if (d.sched) {
                 e->defines.push_back(D("HB_SCHED", d.sched == 3 ? 3 : 1));
                 e->defines.push_back(D("HB_GRP", d.sched == 2 ? 1 : 0));
             }
             return HB_OK;
         }
+        case KIND_SPLITK_REDUCE:
+            if (!d.n || d.n % 4 || d.ksplit < 2 || d.ksplit > 16 || d.out > HB_OUT_RESIDUAL)
+                return fail(HB_ERR_INVALID, "split-K reduce: N a multiple of 4, 2..16 parts");
+            snprintf(name, sizeof name, "gemm_splitk_%u_%s_s%u", d.n, out_tag(d.out), d.ksplit);
+            e->name = name;
+            e->source = "gemm_splitk.hip";
+            e->threads = 256;
+            e->nbind = 3;
+            e->defines = {D("HB_N", d.n), D("HB_OUT", d.out), D("HB_KSPLIT", d.ksplit)};
+            return HB_OK;
         case HB_KIND_GEMM_SIMT:
             if (d.rows_of != HB_ROWS_DENSE || d.out > HB_OUT_RESIDUAL || !d.k || d.k % 16 || !d.n)
                 return fail(HB_ERR_UNSUPPORTED, "gemm_simt: dense rows, K a multiple of 16");
@@ -363,7 +386,11 @@ uint32_t groups_of(const hb_desc& d, uint32_t m) {
             uint32_t bn = d.kind == HB_KIND_GEMM_SIMT ? 64 : d.kind == HB_KIND_GEMM_SWIGLU ? d.bn / 2 : d.bn;
             uint32_t nt = cdiv(d.n, bn);
             if (d.rows_of != HB_ROWS_DENSE) return d.tiles * nt;  // gemm_mma_expert_groups
-            return cdiv(m, bm) * nt;                                 // gemm_mma_groups
+            return cdiv(m, bm) * nt * (d.ksplit > 1 ? d.ksplit : 1);  // gemm_mma_groups
+        }
+        case KIND_SPLITK_REDUCE: {  // 4 outputs a thread, at most 8 workgroups a CU
+            const uint64_t g = ((uint64_t)m * (d.n / 4) + 255) / 256;
+            return (uint32_t)(g < 2048 ? g : 2048);
         }
         case HB_KIND_MATVEC: {  // matvec_groups / matvec_split_groups / matvec_full_groups
             uint32_t rb = d.form == 1 ? 16 : d.rows, per = d.mv_waves / d.split;
@@ -390,6 +417,11 @@ uint32_t groups_of(const hb_desc& d, uint32_t m) {
         default:
             return 0;
     }
+}
+
+uint64_t workspace_of(const hb_desc& d, uint32_t m) {
+    if (d.kind != HB_KIND_GEMM || d.ksplit < 2) return 0;
+    return (uint64_t)d.ksplit * m * d.n * 4;
 }
 
 static int need(const uint64_t* sizes, uint32_t i, uint64_t bytes, const char* what) {
@@ -471,6 +503,10 @@ int check_bindings(const hb_desc& d, const uint64_t* s, uint32_t nbind, uint32_t
             if ((rc = need(s, 2, mm * d.n * 2, "experts"))) return rc;
             if ((rc = need(s, 3, mm * d.n * 2, "shared"))) return rc;
             return need(s, 4, mm * d.n * 2, "x");
+        case KIND_SPLITK_REDUCE:
+            if ((rc = need(s, 0, 16, "state"))) return rc;
+            if ((rc = need(s, 1, (uint64_t)d.ksplit * mm * d.n * 4, "slabs"))) return rc;
+            return need(s, 2, mm * d.n * out_bytes(d.out), "Y");
         case HB_KIND_COMBINE:
             if ((rc = need(s, 0, mm * d.top_k * d.n * 2, "y"))) return rc;
             if ((rc = need(s, 1, mm * k2 * 4, "route"))) return rc;

@@ -56,7 +56,16 @@ struct Kernel {
     Emitted em;
     hipModule_t module = nullptr;
     hipFunction_t fn = nullptr;
+    // A split-K GEMM (desc.ksplit > 1): the kernel that adds its parts'
+    // slabs and applies Out, launched after it by every launch of this one.
+    int32_t reduce = -1;
 };
+
+// The descriptor kind of a split-K GEMM's second kernel (built by the
+// library with its GEMM, never named by a caller).
+constexpr uint32_t KIND_SPLITK_REDUCE = 0xfffe;
+// Workspace bytes a launch of `d` over m rows needs (split-K slabs), 0 if none.
+uint64_t workspace_of(const hb_desc& d, uint32_t m);
 
 }  // namespace hb
 
@@ -79,6 +88,12 @@ struct hb_gpu {
     // The device address of the library's static scratch on this device
     // (hb_static.hip), taken at hb_open.
     void* scratch = nullptr;
+    // The split-K GEMMs' slabs: one workspace for every launch on the
+    // context's stream (launches are in stream order, so one split GEMM's
+    // second kernel has read the slabs before the next GEMM writes them),
+    // grown before a launch that needs more, freed at hb_close.
+    void* ws = nullptr;
+    uint64_t ws_bytes = 0;
 };
 
 namespace hb {

@@ -176,7 +176,22 @@ static int load_kernel(hb_gpu* g, const hb_desc& d, Kernel* k) {
     return HB_OK;
 }
 
-static int launch_raw(hb_gpu* g, const Kernel& k, void** ptrs, uint32_t nptr, uint32_t m,
+// The context's workspace grown to `bytes` (the stream drained first: a
+// launch in flight may still read the old one).
+static int ensure_ws(hb_gpu* g, uint64_t bytes) {
+    if (bytes <= g->ws_bytes) return HB_OK;
+    HB_HIP(hipSetDevice(g->device));
+    HB_HIP(hipStreamSynchronize(g->stream));
+    if (g->ws) HB_HIP(hipFree(g->ws));
+    g->ws = nullptr;
+    g->ws_bytes = 0;
+    const uint64_t sz = (bytes + (1ull << 20) - 1) & ~((1ull << 20) - 1);
+    HB_HIP(hipMalloc(&g->ws, sz));
+    g->ws_bytes = sz;
+    return HB_OK;
+}
+
+static int launch_one(hb_gpu* g, const Kernel& k, void** ptrs, uint32_t nptr, uint32_t m,
                       uint32_t groups) {
     if (groups == 0) return HB_OK;
     // Kernel arguments: the binding pointers, then the launch's row count.
@@ -186,6 +201,21 @@ static int launch_raw(hb_gpu* g, const Kernel& k, void** ptrs, uint32_t nptr, ui
     HB_HIP(hipModuleLaunchKernel(k.fn, groups, 1, 1, k.em.threads, 1, 1, 0, g->stream, args,
                                  nullptr));
     return HB_OK;
+}
+
+// One launch of `k`; a split-K GEMM is two: the parts into the workspace
+// (ensure_ws has sized it), then its reduce from there into Y.
+static int launch_raw(hb_gpu* g, const Kernel& k, void** ptrs, uint32_t nptr, uint32_t m,
+                      uint32_t groups) {
+    if (k.reduce < 0) return launch_one(g, k, ptrs, nptr, m, groups);
+    void* p[10];
+    for (uint32_t i = 0; i < nptr; i++) p[i] = ptrs[i];
+    p[3] = g->ws;
+    int rc = launch_one(g, k, p, nptr, m, groups);
+    if (rc) return rc;
+    const Kernel& r = g->kernels[k.reduce];
+    void* q[3] = {ptrs[0], g->ws, ptrs[3]};
+    return launch_one(g, r, q, 3, m, groups_of(r.desc, m));
 }
 
 int launch_ptrs(hb_gpu* g, int32_t kernel, void* const* ptrs, const uint64_t* sizes, uint32_t nbind,
@@ -198,6 +228,7 @@ int launch_ptrs(hb_gpu* g, int32_t kernel, void* const* ptrs, const uint64_t* si
                                         " bindings given, it takes " + std::to_string(k.em.nbind));
     int rc = check_bindings(k.desc, sizes, nbind, m);
     if (rc) return fail(rc, k.em.name + ": " + hb_last_error());
+    if ((rc = ensure_ws(g, workspace_of(k.desc, m)))) return rc;
     void* p[10];
     for (uint32_t i = 0; i < nbind; i++) p[i] = ptrs[i];
     return launch_raw(g, k, p, nbind, m, groups_of(k.desc, m));
@@ -280,6 +311,7 @@ void hb_close(hb_gpu* g) {
     if (g->zero_kernel.module) hipModuleUnload(g->zero_kernel.module);
     for (auto& b : g->bufs)
         if (b.live) hipFree(b.ptr);
+    if (g->ws) hipFree(g->ws);
     hipEventDestroy(g->ev0);
     hipEventDestroy(g->ev1);
     hipStreamDestroy(g->stream);
@@ -392,6 +424,18 @@ int hb_kernel_build(hb_gpu* g, const hb_desc* desc, int32_t* kernel) {
     Kernel k;
     rc = load_kernel(g, d, &k);
     if (rc) return rc;
+    if (d.kind == HB_KIND_GEMM && d.ksplit > 1) {
+        // Its second kernel, built (or found) first.
+        hb_desc rd{};
+        rd.kind = KIND_SPLITK_REDUCE;
+        rd.n = d.n;
+        rd.out = d.out;
+        rd.ksplit = d.ksplit;
+        if ((rc = hb_kernel_build(g, &rd, &k.reduce))) {
+            hipModuleUnload(k.module);
+            return rc;
+        }
+    }
     g->kernels.push_back(k);
     *kernel = (int32_t)(g->kernels.size() - 1);
     g->by_name[em.name] = *kernel;
@@ -453,6 +497,7 @@ int hb_time_each(hb_gpu* g, const hb_op* ops, uint32_t nops, uint32_t reps, doub
         }
         int rc = check_bindings(k.desc, sizes, op.nbind, op.m);
         if (rc) return fail(rc, k.em.name + ": " + hb_last_error());
+        if ((rc = ensure_ws(g, workspace_of(k.desc, op.m)))) return rc;
         ready[i].k = &k;
         ready[i].n = op.nbind;
         ready[i].m = op.m;

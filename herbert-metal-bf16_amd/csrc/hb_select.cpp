@@ -232,7 +232,7 @@ struct Tune {
 // indexes this table (gemm.mma=1).
 struct Form {
     const char* name;
-    uint32_t bm, bn, bk, wm, wn, mfma, dbuf, dma, order, band, sched;
+    uint32_t bm, bn, bk, wm, wn, mfma, dbuf, dma, order, band, sched, ksplit;
 };
 const Form kForms[10] = {
     {"mma", 128, 128, 64, 2, 2, 16, 1, 1, 1},
@@ -289,6 +289,27 @@ const Form kMoreForms[] = {
     {"pp_t128x160_k64_b4", 128, 160, 64, 4, 2, 16, 3, 1, 1, 4, 1},
     {"pp_t128x288_k64", 128, 288, 64, 4, 2, 16, 2, 1, 1, 0, 1},
 };
+// Split K (hb_desc.ksplit) for the shapes whose tiles fill less than a
+// round of the 256 CUs (M = 512 and 1024, and the narrow N = 2560 outputs
+// at 2048): s workgroups per tile, each over K/s, the f32 parts added by a
+// second kernel.  Forms whose K/s is not a whole count of K tiles are not
+// built for that shape.
+const Form kSplitForms[] = {
+    {"mma_t128x160_s4_ks2", 128, 160, 64, 2, 2, 16, 3, 1, 1, 0, 0, 2},
+    {"mma_t128x160_s4_ks3", 128, 160, 64, 2, 2, 16, 3, 1, 1, 0, 0, 3},
+    {"mma_t128x160_s4_ks4", 128, 160, 64, 2, 2, 16, 3, 1, 1, 0, 0, 4},
+    {"mma_t128x192_w8_s4_ks2", 128, 192, 64, 2, 4, 16, 3, 1, 1, 0, 0, 2},
+    {"mma_t128x192_w8_s4_ks4", 128, 192, 64, 2, 4, 16, 3, 1, 1, 0, 0, 4},
+    {"mma_t128x192_w8_s4_ks8", 128, 192, 64, 2, 4, 16, 3, 1, 1, 0, 0, 8},
+    {"pp_t256x160_k64_ks2", 256, 160, 64, 4, 2, 16, 2, 1, 1, 0, 1, 2},
+    {"pp_t256x160_k64_ks4", 256, 160, 64, 4, 2, 16, 2, 1, 1, 0, 1, 4},
+    {"pp_t128x160_k64_ks2", 128, 160, 64, 4, 2, 16, 3, 1, 1, 0, 1, 2},
+    {"pp_t128x160_k64_ks4", 128, 160, 64, 4, 2, 16, 3, 1, 1, 0, 1, 4},
+    {"pp_t128x256_ks2", 128, 256, 32, 2, 4, 16, 3, 1, 1, 0, 1, 2},
+    {"pp_t128x256_ks4", 128, 256, 32, 2, 4, 16, 3, 1, 1, 0, 1, 4},
+    {"pp_t256x256_ks2", 256, 256, 32, 4, 2, 16, 3, 1, 1, 0, 1, 2},
+    {"pp_t256x256_ks4", 256, 256, 32, 4, 2, 16, 3, 1, 1, 0, 1, 4},
+};
 // The fused [gate | up] + SwiGLU forms (gate_up_pipes, qwen.rs:2148-2193):
 // bn W rows per tile = bn/2 features.
 const Form kFusedForms[] = {
@@ -317,6 +338,7 @@ hb_desc form_desc(const Form& f, uint32_t k, uint32_t n, uint32_t out, bool mf) 
     d.order = f.order;
     d.band = f.band;
     d.sched = f.sched;
+    d.ksplit = f.ksplit;
     return d;
 }
 
@@ -658,6 +680,8 @@ std::vector<std::pair<std::string, hb_desc>> gemm_candidates(hb_engine* e, uint3
     std::vector<std::pair<std::string, hb_desc>> v;
     for (const auto& f : kForms) v.emplace_back(f.name, form_desc(f, k, n, out, mf));
     for (const auto& f : kMoreForms) v.emplace_back(f.name, form_desc(f, k, n, out, mf));
+    for (const auto& f : kSplitForms)
+        if (k % (f.bk * f.ksplit) == 0) v.emplace_back(f.name, form_desc(f, k, n, out, mf));
     for (auto tm_tn : {std::make_pair(64u, 64u), std::make_pair(64u, 32u), std::make_pair(32u, 64u),
                        std::make_pair(32u, 32u), std::make_pair(64u, 16u), std::make_pair(32u, 16u)}) {
         char nm[32];

@@ -35,7 +35,14 @@
 // residual), HB_ROWS (0 dense, 1 gather, 2 scatter, 3 sorted: row p of X
 // and of Y, the rows a gather put in sorted order), HB_TOPK, HB_BM, HB_BN,
 // HB_BK, HB_WM, HB_WN, HB_MFMA (16|32), HB_STAGES (1..4), HB_SWZ, HB_ORDER,
-// HB_MFIRST, HB_DMA, HB_SWIGLU, HB_BAND (the tile order band).
+// HB_MFIRST, HB_DMA, HB_SWIGLU, HB_BAND (the tile order band), HB_KSPLIT.
+//
+// HB_KSPLIT s > 1 (dense rows, f32 out): K cut into s equal parts; the
+// launch holds s workgroups per tile (part = the slow index of the tile
+// walk, so each XCD's contiguous range is mostly one part's tiles), and part
+// p writes its f32 sums over K tiles p*KT .. p*KT + KT - 1 to slab p of Y,
+// [m_launch][N] floats each.  A second kernel (gemm_splitk.hip) adds the
+// slabs and applies Out.
 //
 // HB_SWIGLU 1 (dense or gathered rows, Bf16): the [gate | up] projection and
 // the SwiGLU in one (prefill.rs:755-824, gemm_nax_swiglu; for the experts,
@@ -65,7 +72,11 @@ constexpr u32 IM = TM / FM, IN = TN / FM;
 constexpr u32 CH = BK / 8;                  // 16-byte chunks of a staged row
 constexpr u32 KS = FM == 16 ? 32 : 16;      // K of one MFMA
 constexpr u32 S = BK / KS;                  // MFMA steps per staged tile
-constexpr u32 KT = K / BK;
+#ifndef HB_KSPLIT
+#define HB_KSPLIT 1
+#endif
+constexpr u32 KSP = HB_KSPLIT;
+constexpr u32 KT = K / BK / KSP;            // K tiles of one part
 #ifndef HB_SWIGLU
 #define HB_SWIGLU 0
 #endif
@@ -84,7 +95,9 @@ constexpr u32 X_LD = (XCH + NT - 1) / NT, W_LD = (WCH + NT - 1) / NT;
 constexpr u32 XCHP = HB_DMA ? X_LD * NT : XCH, WCHP = HB_DMA ? W_LD * NT : WCH;
 constexpr u32 NS = HB_STAGES;
 
-static_assert(K % BK == 0, "K a multiple of the K step");
+static_assert(K % (BK * KSP) == 0, "K a multiple of the K step times the parts");
+static_assert(KSP == 1 || (ROWS == 0 && OUT == 1 && HB_SWIGLU == 0),
+              "split K: dense rows, f32 partial sums");
 static_assert(N % 4 == 0, "N a multiple of 4");
 static_assert(TM % FM == 0 && TN % FM == 0, "wave tile a multiple of the MFMA block");
 static_assert(BK % KS == 0 && (CH & (CH - 1)) == 0, "K step");
@@ -183,6 +196,9 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     } else if (HB_ORDER == 1) {
         g = xcd_remap(g, gridDim.x);
     }
+    // Split K: part = the slow index; g the tile within the part.
+    const u32 part = KSP > 1 ? g / (gridDim.x / KSP) : 0;
+    if constexpr (KSP > 1) g -= part * (gridDim.x / KSP);
 
     // The tile: its first row (dense row or sorted pair), its rows, its
     // column tile and its expert.
@@ -265,7 +281,7 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     for (u32 q = 0; q < X_LD; q++) {
         const u32 p = tid + q * NT, r = p / CH;
         const u32 cc = HB_DMA ? ((p % CH) ^ ((r >> HB_SWZ) & (CH - 1))) : p % CH;
-        xoff[q] = x_row(r) * K + cc * 8;
+        xoff[q] = x_row(r) * K + part * (KT * BK) + cc * 8;
         // Direct-to-LDS: rows past the tile's (never stored) at a byte
         // offset past the buffer resource's range (0x7fffffff bytes), so
         // the load writes zeros to LDS without a memory access.
@@ -275,7 +291,7 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     for (u32 q = 0; q < W_LD; q++) {
         const u32 p = tid + q * NT, r = p / CH;
         const u32 cc = HB_DMA ? ((p % CH) ^ ((r >> HB_SWZ) & (CH - 1))) : p % CH;
-        woff[q] = w_row(r) * K + cc * 8;
+        woff[q] = w_row(r) * K + part * (KT * BK) + cc * 8;
     }
 
     acc_t acc[IN][IM];
@@ -484,6 +500,7 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     }
 #endif
 
+    if constexpr (KSP > 1) Yv = (float*)Yv + (u64)part * m_launch * N;  // this part's slab
 #if HB_DMA
     if constexpr (EPI_VIA_LDS) {
         epilogue_lds(lds, acc, tid, wm, wn, fr, fc, row0, rows, n0, Yv);

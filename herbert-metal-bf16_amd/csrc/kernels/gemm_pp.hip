@@ -64,7 +64,9 @@
 // residual), HB_BM, HB_BN, HB_BK, HB_WM, HB_WN (WM * WN = 8), HB_MFMA (16|32),
 // HB_STAGES (3|4), HB_SWZ, HB_ORDER, HB_MFIRST, HB_BAND, HB_SCHED (1 | 3),
 // HB_GRP (ping-pong: which waves form a group: 0 waves 0-3 / 4-7, 1 even /
-// odd waves).
+// odd waves), HB_KSPLIT (s > 1: K cut into s parts, part p's f32 sums into
+// slab p of Y, [m_launch][N] floats each, as in gemm_mfma.hip; a second
+// kernel adds the slabs).
 //
 // Bindings: state (u32[4], state[3] = rows), W, X, Y, list, tiles (unused:
 // dense rows); then the rows the launch was sized for (m_launch).
@@ -84,7 +86,11 @@ constexpr u32 IM = TM / FM, IN = TN / FM;
 constexpr u32 CH = BK / 8;                 // 16-byte chunks of a staged row
 constexpr u32 KS = FM == 16 ? 32 : 16;     // K of one MFMA
 constexpr u32 S = BK / KS;                 // MFMA steps per K tile
-constexpr u32 KT = K / BK;
+#ifndef HB_KSPLIT
+#define HB_KSPLIT 1
+#endif
+constexpr u32 KSP = HB_KSPLIT;
+constexpr u32 KT = K / BK / KSP;           // K tiles of one part
 constexpr u32 NS = HB_STAGES;
 constexpr u32 NTILES = (N + BN - 1) / BN;
 constexpr u32 XST = BM * CH, WST = BN * CH;  // chunks per stage
@@ -103,7 +109,8 @@ constexpr u32 LMIN = NXL / NWV + NWL / NWV;  // loads per stage of every wave
 
 static_assert(HB_SCHED == 1 || HB_SCHED == 3, "schedule 1 or 3");
 static_assert(WM * WN == NWV, "eight wavefronts (ping-pong) or four");
-static_assert(K % BK == 0, "K a multiple of the K step");
+static_assert(K % (BK * KSP) == 0, "K a multiple of the K step times the parts");
+static_assert(KSP == 1 || OUT == 1, "split K: f32 partial sums");
 static_assert(N % 4 == 0, "N a multiple of 4");
 static_assert(TM % FM == 0 && TN % FM == 0, "wave tile a multiple of the MFMA block");
 static_assert(BK % KS == 0 && (CH & (CH - 1)) == 0, "K step");
@@ -176,6 +183,9 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     // bands of row tiles (nax_tile_order).
     u32 g = blockIdx.x;
     if (HB_ORDER == 1) g = xcd_remap(g, gridDim.x);
+    // Split K: part = the slow index; g the tile within the part.
+    const u32 part = KSP > 1 ? g / (gridDim.x / KSP) : 0;
+    if constexpr (KSP > 1) g -= part * (gridDim.x / KSP);
     const u32 m = rows_of_state(state, m_launch);
     const u32 mb = (m + BM - 1) / BM;
     u32 gm, gn;
@@ -210,14 +220,14 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     for (u32 i = 0; i < XLMAX; i++) {
         const u32 p = (wave + NWV * i) * 64 + lane, r = p / CH;
         const u32 cc = (p % CH) ^ ((r >> HB_SWZ) & (CH - 1));
-        xoff[i] = r < rows && r < BM ? ((row0 + r) * K + cc * 8) * 2 : 0x80000000u;
+        xoff[i] = r < rows && r < BM ? ((row0 + r) * K + part * (KT * BK) + cc * 8) * 2 : 0x80000000u;
     }
 #pragma unroll
     for (u32 i = 0; i < WLMAX; i++) {
         const u32 p = (wave + NWV * i) * 64 + lane, r = p / CH;
         const u32 cc = (p % CH) ^ ((r >> HB_SWZ) & (CH - 1));
         const u32 n = n0 + r;
-        woff[i] = ((n < N ? n : N - 1) * K + cc * 8) * 2;
+        woff[i] = ((n < N ? n : N - 1) * K + part * (KT * BK) + cc * 8) * 2;
     }
 
     const __amdgpu_buffer_rsrc_t rX =
@@ -383,6 +393,7 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     step(KT - 1, st, 1, bconst<false>{});
     }
 
+    if constexpr (KSP > 1) Yv = (float*)Yv + (u64)part * m_launch * N;  // this part's slab
     if constexpr (EPI_LDS) {
         epilogue_lds(lds, acc, tid, wm, wn, fr, fc, row0, rows, n0, Yv);
         return;

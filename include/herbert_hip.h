@@ -173,6 +173,13 @@ typedef struct hb_desc {
      * fragments from LDS between its MFMAs (3 or 4 stages, an even count of
      * K tiles). */
     uint32_t sched;
+    /* MFMA GEMM (dense rows, direct-to-LDS, sched 0), 0 or 1 = no split: K
+     * cut into `ksplit` equal parts, one workgroup per (tile, part) writing
+     * its f32 sums to a workspace the context owns, then a second kernel
+     * adding the parts in order 0..ksplit-1 and applying Out -- for shapes
+     * whose tiles fill less than a round of the CUs.  One launch handle:
+     * hb_launch / hb_time run both kernels. */
+    uint32_t ksplit;
 } hb_desc;
 
 /* Gpu::pipeline(&Emitted) (metal/gpu.rs:127-148) for the kernel the

@@ -50,6 +50,20 @@ TILES = {
     "il_t256x256": dict(bm=256, bn=256, bk=32, wm=2, wn=2, mfma=16, dbuf=3, lds_dma=1, order=1, sched=3),
     "il_t256x192_s3": dict(bm=256, bn=192, bk=32, wm=2, wn=2, mfma=16, dbuf=2, lds_dma=1, order=1,
                            sched=3),
+    # split K (hb_desc.ksplit): the parts' f32 sums added by a second kernel
+    "ks2_t128x128": dict(bm=128, bn=128, bk=64, wm=2, wn=2, mfma=16, dbuf=1, lds_dma=1, order=1, ksplit=2),
+    "ks4_t128x160_s4": dict(bm=128, bn=160, bk=64, wm=2, wn=2, mfma=16, dbuf=3, lds_dma=1, order=1,
+                            ksplit=4),
+    "ks2_t256x192_w8_b4": dict(bm=256, bn=192, bk=64, wm=4, wn=2, mfma=16, dbuf=1, lds_dma=1, order=1,
+                               band=4, ksplit=2),
+    "ks2_pp_t128x256": dict(bm=128, bn=256, bk=32, wm=2, wn=4, mfma=16, dbuf=3, lds_dma=1, order=1,
+                            sched=1, ksplit=2),
+    "ks4_pp_t256x160_k64": dict(bm=256, bn=160, bk=64, wm=4, wn=2, mfma=16, dbuf=2, lds_dma=1, order=1,
+                                sched=1, ksplit=4),
+    "ks2_il_t256x192": dict(bm=256, bn=192, bk=32, wm=2, wn=2, mfma=16, dbuf=2, lds_dma=1, order=1,
+                            sched=3, ksplit=2),
+    "ks4_t64x128_reg": dict(bm=64, bn=128, bk=64, wm=2, wn=2, mfma=16, dbuf=1, lds_dma=0, order=0,
+                            ksplit=4),
 }
 
 
@@ -119,6 +133,47 @@ def test_gemm_state_rows_below_launch_rows(gpu):
         gpu.free(b)
     assert np.all(got[100:] == 0)
     check_close(got[:100], orc.gemm(x[:100], w), k, abs_products(x[:100], w), "state rows")
+
+
+@pytest.mark.parametrize("ksplit", [2, 3])
+def test_gemm_split_k_state_rows_below_launch_rows(gpu, ksplit):
+    """Split K with state[3] < the launch's m: the parts' slabs are the
+    launch's rows apart, only state[3] rows are added and written; Out
+    Residual adds to Y once."""
+    m, k, n = 300, 768, 640
+    x, w = inputs(m, k, n, 14)
+    y0 = hb.normal_bf16(15, 1.0, (m, n))
+    got = run_gemm(gpu, x, w, 2, y0, m=m, **dict(TILES["ks2_t128x128"], ksplit=ksplit))
+    check_close(got, orc.gemm(x, w, 2, y0), k, abs_products(x, w), "split rows m",
+                acc=orc.gemm(x, w, orc.OUT_F32))
+    st = gpu.alloc_with(np.array([0, 0, 0, 100], np.uint32))
+    W, X = gpu.alloc_with(w), gpu.alloc_with(x)
+    Y = gpu.alloc_with(y0)
+    kern = gpu.pipeline(hb.gemm_mma(k, n, 2, **dict(TILES["ks2_t128x128"], ksplit=ksplit)))
+    assert gpu.kernel_name(kern).endswith("_ks%d" % ksplit)
+    gpu.launch(kern, [hb.r(st), hb.r(W), hb.r(X), hb.r(Y), hb.r(st), hb.r(st)], m)
+    got = gpu.download(Y, np.uint16, m * n).reshape(m, n)
+    for b in (st, W, X, Y):
+        gpu.free(b)
+    assert np.array_equal(got[100:], y0[100:])
+    check_close(got[:100], orc.gemm(x[:100], w, 2, y0[:100]), k, abs_products(x[:100], w),
+                "split state rows", acc=orc.gemm(x[:100], w, orc.OUT_F32))
+
+
+def test_gemm_split_k_is_deterministic_and_refused_where_unsplittable(gpu):
+    """The parts are added in a fixed order: two launches give the same bits.
+    K not a multiple of bk x parts, expert rows and the pipelined schedules
+    are refused."""
+    m, k, n = 512, 1024, 3584
+    x, w = inputs(m, k, n, 16)
+    a = run_gemm(gpu, x, w, 0, **TILES["ks4_t128x160_s4"])
+    b = run_gemm(gpu, x, w, 0, **TILES["ks4_t128x160_s4"])
+    assert np.array_equal(a, b)
+    for bad in (dict(TILES["ks2_t128x128"], ksplit=3),
+                dict(TILES["ks2_t128x128"], ksplit=17),
+                dict(TILES["il_t256x192_s3"], ksplit=32)):
+        with pytest.raises(hb.HerbertError):
+            gpu.pipeline(hb.gemm_mma(k, n, 0, **bad))
 
 
 @pytest.mark.parametrize("band", [1, 2, 3])
