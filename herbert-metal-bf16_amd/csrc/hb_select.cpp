@@ -830,6 +830,129 @@ int hb_engine_matvec(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, uint32_
                                   hb_range{}, kernel);
 }
 
+// The matvec candidates of mv_full's timed choice (qwen.rs:1311-1511), in
+// order, for one shape, m, fusion and the tune's splits and persistent
+// counts.
+std::vector<std::pair<std::string, hb_desc>> mv_candidates(hb_engine* e, uint32_t k, uint32_t n,
+                                                           uint32_t out, uint32_t xsrc,
+                                                           uint32_t eps_bits, uint32_t plus_one,
+                                                           uint32_t mv_m) {
+    const Tune& t = e->t;
+    const bool fused = xsrc != HB_XSRC_PLAIN || out == HB_OUT_SWIGLU;
+    auto desc = [&](uint32_t form, uint32_t rows, uint32_t split, uint32_t persist) {
+        hb_desc d{};
+        d.kind = HB_KIND_MATVEC;
+        d.k = k;
+        d.n = n;
+        d.out = out;
+        d.mv_m = mv_m;
+        d.form = form;
+        d.rows = rows;
+        d.split = split;
+        d.persist = persist;
+        d.unroll = 4;
+        d.xsrc = xsrc;
+        d.eps_bits = eps_bits;
+        d.plus_one = plus_one;
+        return d;
+    };
+    std::vector<std::pair<std::string, hb_desc>> v;
+    std::vector<uint32_t> splits = t["mv.splitauto"] ? std::vector<uint32_t>{1, 2, 4} : std::vector<uint32_t>{1};
+    std::vector<uint32_t> pers = {0};
+    for (uint32_t p : t.mv_persists) pers.push_back(p);
+    // XSrc::Norm computes the norm once per workgroup: persistent
+    // workgroups (two and four per CU) amortise it unless mv.persists names
+    // its own counts.
+    if (xsrc == HB_XSRC_NORM && t.mv_persists.empty())
+        for (uint32_t p : {512u, 1024u}) pers.push_back(p);
+    for (uint32_t split : splits)
+        for (uint32_t p : pers)
+            for (uint32_t rows : {1u, 2u, 4u, 8u}) {
+                if (rows * mv_m > 64 || (p > 0 && rows == 8)) continue;
+                if (out == HB_OUT_SWIGLU && rows < 2) continue;
+                std::string tag = (split > 1 ? "k" + std::to_string(split) : "") +
+                                  (p ? "p" + std::to_string(p) : "");
+                v.emplace_back("r" + std::to_string(rows) + tag, desc(0, rows, split, p));
+                v.emplace_back("d" + std::to_string(rows) + tag, desc(2, rows, split, p));
+                if (rows <= 2) {
+                    // A whole row's chunks in one batch of loads when K /
+                    // split <= 4096: one HBM latency per wave, not two.
+                    hb_desc d8 = desc(mv_m > 1 ? 2 : 0, rows, split, p);
+                    d8.unroll = 8;
+                    v.emplace_back((mv_m > 1 ? "d" : "r") + std::to_string(rows) + tag + "u8", d8);
+                }
+            }
+    // The x rows staged in LDS once per workgroup (plain or XSrc::Swiglu,
+    // m*K*2 <= 64 KiB): for several rows, where reloading x per row block
+    // through the vector memory path costs more than the W stream, and for
+    // XSrc::Swiglu, whose SwiGLU is then computed once per workgroup.
+    // Persistent workgroups (two and four per CU) stage it fewer times.
+    if ((mv_m > 1 || xsrc == HB_XSRC_SWIGLU) && xsrc != HB_XSRC_NORM && (uint64_t)mv_m * k * 2 <= 65536)
+        for (uint32_t p : {0u, 512u, 1024u})
+            for (uint32_t rows : {1u, 2u, 4u}) {
+                if (rows * mv_m > 64 || (out == HB_OUT_SWIGLU && rows < 2)) continue;
+                hb_desc dx = desc(mv_m > 1 ? 2 : 0, rows, 1, p);
+                dx.unroll = 8;
+                dx.x_lds = 1;
+                v.emplace_back((mv_m > 1 ? "d" : "r") + std::to_string(rows) + (p ? "p" + std::to_string(p) : "") + "u8xl", dx);
+            }
+    // For several rows, x staged once per CU by one 16-wave workgroup (or
+    // two 8-wave ones) with up to 144 KiB of LDS: the long-K o and down
+    // shapes, whose x the 4-wave workgroups cannot hold or would stage per
+    // four waves (measured at m=8: down 2.6 -> 3.5 TB/s, o 2.1 -> 2.5).
+    if (mv_m > 1 && xsrc != HB_XSRC_NORM && (uint64_t)mv_m * k * 2 <= 147456) {
+        const bool small = (uint64_t)mv_m * k * 2 <= 65536;
+        const uint32_t r1 = out == HB_OUT_SWIGLU ? 2 : 1;
+        struct W { uint32_t waves, rows, persist, unroll; };
+        for (W w : {W{16, r1, 0, 8}, W{16, r1, 256, 4}, W{16, r1, 256, 8}, W{8, 2, 256, 4}}) {
+            if (!small && w.persist != 256) continue;  // one workgroup per CU
+            if (w.rows * mv_m > 64) continue;
+            hb_desc dw = desc(2, w.rows, 1, w.persist);
+            dw.unroll = w.unroll;
+            dw.x_lds = 1;
+            dw.mv_waves = w.waves;
+            v.emplace_back("d" + std::to_string(w.rows) + (w.persist ? "p" + std::to_string(w.persist) : "") + "u" +
+                    std::to_string(w.unroll) + "xl_w" + std::to_string(w.waves), dw);
+        }
+    }
+    // The MFMA arithmetic with W read in row order through a wave-private
+    // LDS tile (form 3): for several rows, where the VALU forms run out of
+    // issue (measured at m=8: gate_up 4.4 -> 5.0 TB/s, lm_head 5.3 -> 6.1).
+    if (mv_m > 1 && !fused && k % 128 == 0) {
+        // rows 32: two 16-row tiles per wave share each x fragment (half
+        // the x loads per W byte; lm_head at m=8: 6.1 -> 6.7 TB/s).
+        struct F { uint32_t unroll, split, persist, rows; };
+        for (F f : {F{4, 4, 0, 16}, F{4, 2, 0, 16}, F{4, 1, 512, 16}, F{4, 4, 512, 16}, F{8, 2, 0, 16},
+                    F{8, 4, 0, 16}, F{8, 4, 512, 16}, F{4, 4, 0, 32}, F{4, 4, 512, 32}}) {
+            hb_desc d3 = desc(3, f.rows, f.split, f.persist);
+            d3.unroll = f.unroll;
+            v.emplace_back("mfl" + std::string(f.rows == 32 ? "_r32" : "") + "_u" + std::to_string(f.unroll) + "k" +
+                    std::to_string(f.split) + (f.persist ? "p" + std::to_string(f.persist) : ""), d3);
+        }
+    }
+    for (uint32_t split : splits)
+        for (uint32_t p : pers) {
+            if (fused) break;  // the fusions are VALU forms
+            std::string tag = (split > 1 ? "k" + std::to_string(split) : "") + (p ? "p" + std::to_string(p) : "");
+            v.emplace_back("mfma" + tag, desc(1, 16, split, p));
+            for (uint32_t u : {8u, 16u}) {
+                hb_desc du = desc(1, 16, split, p);
+                du.unroll = u;
+                v.emplace_back("mfma_u" + std::to_string(u) + tag, du);
+            }
+        }
+    return v;
+}
+
+int hb_engine_matvec_candidates(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, uint32_t xsrc,
+                                uint32_t eps_bits, uint32_t plus_one, uint32_t mv_m, hb_desc* descs,
+                                uint32_t cap, uint32_t* count) {
+    const auto v = mv_candidates(e, k, n, out, xsrc, eps_bits, plus_one, mv_m);
+    *count = (uint32_t)v.size();
+    for (uint32_t i = 0; i < v.size() && i < cap; i++) descs[i] = v[i].second;
+    return HB_OK;
+}
+
 int hb_engine_matvec_fused(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, uint32_t xsrc,
                            uint32_t eps_bits, uint32_t plus_one, uint32_t mv_m, const hb_range* ws,
                            uint32_t nws, hb_range x, hb_range y, hb_range norm_w, int32_t* kernel) {
@@ -884,14 +1007,6 @@ int hb_engine_matvec_fused(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, u
     uint32_t nw = t["mv.cold"] ? nws : 1;
     std::vector<Cand> c;
     std::vector<hb_desc> descs;
-    std::vector<uint32_t> splits = t["mv.splitauto"] ? std::vector<uint32_t>{1, 2, 4} : std::vector<uint32_t>{1};
-    std::vector<uint32_t> pers = {0};
-    for (uint32_t p : t.mv_persists) pers.push_back(p);
-    // XSrc::Norm computes the norm once per workgroup: persistent
-    // workgroups (two and four per CU) amortise it unless mv.persists names
-    // its own counts.
-    if (xsrc == HB_XSRC_NORM && t.mv_persists.empty())
-        for (uint32_t p : {512u, 1024u}) pers.push_back(p);
     auto add = [&](const std::string& name, const hb_desc& d) {
         int32_t kk;
         if (e->build(d, &kk)) {
@@ -903,82 +1018,8 @@ int hb_engine_matvec_fused(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, u
         c.push_back({name, kk, ops});
         descs.push_back(d);
     };
-    for (uint32_t split : splits)
-        for (uint32_t p : pers)
-            for (uint32_t rows : {1u, 2u, 4u, 8u}) {
-                if (rows * mv_m > 64 || (p > 0 && rows == 8)) continue;
-                if (out == HB_OUT_SWIGLU && rows < 2) continue;
-                std::string tag = (split > 1 ? "k" + std::to_string(split) : "") +
-                                  (p ? "p" + std::to_string(p) : "");
-                add("r" + std::to_string(rows) + tag, desc(0, rows, split, p));
-                add("d" + std::to_string(rows) + tag, desc(2, rows, split, p));
-                if (rows <= 2) {
-                    // A whole row's chunks in one batch of loads when K /
-                    // split <= 4096: one HBM latency per wave, not two.
-                    hb_desc d8 = desc(mv_m > 1 ? 2 : 0, rows, split, p);
-                    d8.unroll = 8;
-                    add((mv_m > 1 ? "d" : "r") + std::to_string(rows) + tag + "u8", d8);
-                }
-            }
-    // The x rows staged in LDS once per workgroup (plain or XSrc::Swiglu,
-    // m*K*2 <= 64 KiB): for several rows, where reloading x per row block
-    // through the vector memory path costs more than the W stream, and for
-    // XSrc::Swiglu, whose SwiGLU is then computed once per workgroup.
-    // Persistent workgroups (two and four per CU) stage it fewer times.
-    if ((mv_m > 1 || xsrc == HB_XSRC_SWIGLU) && xsrc != HB_XSRC_NORM && (uint64_t)mv_m * k * 2 <= 65536)
-        for (uint32_t p : {0u, 512u, 1024u})
-            for (uint32_t rows : {1u, 2u, 4u}) {
-                if (rows * mv_m > 64 || (out == HB_OUT_SWIGLU && rows < 2)) continue;
-                hb_desc dx = desc(mv_m > 1 ? 2 : 0, rows, 1, p);
-                dx.unroll = 8;
-                dx.x_lds = 1;
-                add((mv_m > 1 ? "d" : "r") + std::to_string(rows) + (p ? "p" + std::to_string(p) : "") + "u8xl", dx);
-            }
-    // For several rows, x staged once per CU by one 16-wave workgroup (or
-    // two 8-wave ones) with up to 144 KiB of LDS: the long-K o and down
-    // shapes, whose x the 4-wave workgroups cannot hold or would stage per
-    // four waves (measured at m=8: down 2.6 -> 3.5 TB/s, o 2.1 -> 2.5).
-    if (mv_m > 1 && xsrc != HB_XSRC_NORM && (uint64_t)mv_m * k * 2 <= 147456) {
-        const bool small = (uint64_t)mv_m * k * 2 <= 65536;
-        const uint32_t r1 = out == HB_OUT_SWIGLU ? 2 : 1;
-        struct W { uint32_t waves, rows, persist, unroll; };
-        for (W w : {W{16, r1, 0, 8}, W{16, r1, 256, 4}, W{16, r1, 256, 8}, W{8, 2, 256, 4}}) {
-            if (!small && w.persist != 256) continue;  // one workgroup per CU
-            if (w.rows * mv_m > 64) continue;
-            hb_desc dw = desc(2, w.rows, 1, w.persist);
-            dw.unroll = w.unroll;
-            dw.x_lds = 1;
-            dw.mv_waves = w.waves;
-            add("d" + std::to_string(w.rows) + (w.persist ? "p" + std::to_string(w.persist) : "") + "u" +
-                    std::to_string(w.unroll) + "xl_w" + std::to_string(w.waves), dw);
-        }
-    }
-    // The MFMA arithmetic with W read in row order through a wave-private
-    // LDS tile (form 3): for several rows, where the VALU forms run out of
-    // issue (measured at m=8: gate_up 4.4 -> 5.0 TB/s, lm_head 5.3 -> 6.1).
-    if (mv_m > 1 && !fused && k % 128 == 0) {
-        // rows 32: two 16-row tiles per wave share each x fragment (half
-        // the x loads per W byte; lm_head at m=8: 6.1 -> 6.7 TB/s).
-        struct F { uint32_t unroll, split, persist, rows; };
-        for (F f : {F{4, 4, 0, 16}, F{4, 2, 0, 16}, F{4, 1, 512, 16}, F{4, 4, 512, 16}, F{8, 2, 0, 16},
-                    F{8, 4, 0, 16}, F{8, 4, 512, 16}, F{4, 4, 0, 32}, F{4, 4, 512, 32}}) {
-            hb_desc d3 = desc(3, f.rows, f.split, f.persist);
-            d3.unroll = f.unroll;
-            add("mfl" + std::string(f.rows == 32 ? "_r32" : "") + "_u" + std::to_string(f.unroll) + "k" +
-                    std::to_string(f.split) + (f.persist ? "p" + std::to_string(f.persist) : ""), d3);
-        }
-    }
-    for (uint32_t split : splits)
-        for (uint32_t p : pers) {
-            if (fused) break;  // the fusions are VALU forms
-            std::string tag = (split > 1 ? "k" + std::to_string(split) : "") + (p ? "p" + std::to_string(p) : "");
-            add("mfma" + tag, desc(1, 16, split, p));
-            for (uint32_t u : {8u, 16u}) {
-                hb_desc du = desc(1, 16, split, p);
-                du.unroll = u;
-                add("mfma_u" + std::to_string(u) + tag, du);
-            }
-        }
+    for (const auto& cd : mv_candidates(e, k, n, out, xsrc, eps_bits, plus_one, mv_m))
+        add(cd.first, cd.second);
     if (c.empty()) return fail(HB_ERR_COMPILE, std::string("matvec ") + key + ": no form built");
     std::vector<bool> all(c.size(), true);
     size_t best;

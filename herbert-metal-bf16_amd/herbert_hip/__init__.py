@@ -24,6 +24,7 @@ back to the CPU: without libherbert_hip.so, importing the package raises.
 """
 import ctypes
 import enum
+import struct
 import os
 
 import numpy as np
@@ -200,6 +201,8 @@ lib.hb_engine_experts.argtypes = [_P, _u32, _u32, _u32, _u32, _u32, ctypes.POINT
                                   ctypes.POINTER(_i32), ctypes.POINTER(_u32)]
 lib.hb_engine_gemm_candidates.argtypes = [_P, _u32, _u32, _u32, ctypes.POINTER(Desc), _u32,
                                           ctypes.POINTER(_u32)]
+lib.hb_engine_matvec_candidates.argtypes = [_P, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
+                                            ctypes.POINTER(Desc), _u32, ctypes.POINTER(_u32)]
 lib.hb_moe_experts_run.argtypes = [_P, ctypes.POINTER(_i32), _i32, _i32, ctypes.POINTER(MoeIo), Range,
                                    _u32]
 lib.hb_engine_tune_get.argtypes = [_P, ctypes.c_char_p, ctypes.POINTER(_u32)]
@@ -481,6 +484,16 @@ class Engine:
         arr = (Desc * cap)()
         cnt = _u32()
         check(lib.hb_engine_gemm_candidates(self.h, k, n, int(out), arr, cap, ctypes.byref(cnt)))
+        return [arr[i].replace() for i in range(min(cnt.value, cap))]
+
+    def matvec_candidates(self, k, n, out, mv_m, xsrc=0, eps=0.0, plus_one=False):
+        """The descriptors mv_full times for a k x n matvec of mv_m rows, in order."""
+        cap = 256
+        arr = (Desc * cap)()
+        cnt = _u32()
+        eps_bits = struct.unpack("<I", struct.pack("<f", eps))[0]
+        check(lib.hb_engine_matvec_candidates(self.h, k, n, int(out), int(xsrc), eps_bits, int(plus_one),
+                                              mv_m, arr, cap, ctypes.byref(cnt)))
         return [arr[i].replace() for i in range(min(cnt.value, cap))]
 
     def gemm(self, k, n, out, state, w, x, y, m):

@@ -300,6 +300,14 @@ int hb_engine_matvec(hb_engine *engine, uint32_t k, uint32_t n, uint32_t out, ui
 int hb_engine_matvec_fused(hb_engine *engine, uint32_t k, uint32_t n, uint32_t out, uint32_t xsrc,
                            uint32_t eps_bits, uint32_t plus_one, uint32_t mv_m, const hb_range *ws,
                            uint32_t nws, hb_range x, hb_range y, hb_range norm_w, int32_t *kernel);
+/* The descriptors mv_full (qwen.rs:1311-1511) times for a k x n matvec of
+ * mv_m rows written as `out`, with XSrc `xsrc` (eps_bits, plus_one for
+ * XSrc::Norm), in candidate order; *count = how many, the first
+ * min(count, cap) written.  The timed choice checks no candidate, so a
+ * caller can check every kernel it can pick. */
+int hb_engine_matvec_candidates(hb_engine *engine, uint32_t k, uint32_t n, uint32_t out,
+                                uint32_t xsrc, uint32_t eps_bits, uint32_t plus_one, uint32_t mv_m,
+                                hb_desc *descs, uint32_t cap, uint32_t *count);
 
 /* QwenEngine::expert_pipes (qwen.rs:2326-2391): the sort, the grouped
  * gate_up GEMM (Gather) and down GEMM (Scatter) of an MoE layer of `experts`

@@ -84,7 +84,7 @@ def gemm(x, w, out=OUT_BF16, y=None, threads=None):
     if out == OUT_F32:
         res = np.zeros((m, n), np.float32)
     elif out == OUT_RESIDUAL:
-        res = np.array(y, dtype=np.uint16, copy=True).reshape(m, n)
+        res = np.array(y, dtype=np.uint16, order="C", copy=True).reshape(m, n)
     else:
         res = np.zeros((m, n), np.uint16)
     lib.hbo_gemm(_p(x), _p(w), _p(res), m, k, n, out, threads or threads_default())
@@ -170,7 +170,7 @@ lib.hbo_moe_out.argtypes = [_P, _P, _P, _P, _P, ctypes.c_int, ctypes.c_int, ctyp
 def moe_out(xn, gate, ex, sh, x, order=0):
     """moe_out (hb_oracle.c hbo_moe_out): the updated x (a copy)."""
     xn, gate, ex, sh = (_c(a, np.uint16) for a in (xn, gate, ex, sh))
-    out = np.array(x, dtype=np.uint16, copy=True)
+    out = np.array(x, dtype=np.uint16, order="C", copy=True)
     rows, d = out.shape
     lib.hbo_moe_out(_p(xn), _p(gate), _p(ex), _p(sh), _p(out), rows, d, order)
     return out

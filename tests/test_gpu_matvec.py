@@ -63,8 +63,8 @@ def test_matvec_config3_layer(gpu, name, k, n, out, form, m):
     check_close(got, want, k, abs_products(x, w), "%s %s m=%d" % (name, form, m), acc=acc)
 
 
-@pytest.mark.parametrize("m", [1, 8])
-@pytest.mark.parametrize("form", ["valu_r4", "dot2_r2", "mfma_k1", "mfl_u4_k4"])
+@pytest.mark.parametrize("m", [1, 4, 8])
+@pytest.mark.parametrize("form", ["valu_r4", "dot2_r2", "mfma_k1", "mfl_u4_k4", "mfl_r32_u4_k4"])
 def test_matvec_lm_head(gpu, form, m):
     """lm_head K=2560, N=151936 (778 MB of weights), all outputs checked."""
     k, n = 2560, 151936

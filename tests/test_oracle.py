@@ -478,3 +478,20 @@ def test_moe_out_closed_forms():
         ref = g64[:, None] * bf16_to_f32(sh).astype(np.float64)
         ulp = 2.0 ** (np.floor(np.log2(np.maximum(np.abs(ref), 2.0 ** -126))) - 7)
         assert np.all(np.abs(bf16_to_f32(got) - ref) <= 3 * ulp)
+
+
+def test_residual_input_layout_does_not_matter():
+    """Out::Residual's y may be any numpy view (a column selection is not C
+    ordered): the oracle reads it in row order either way."""
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((4, 64)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    w = (rng.standard_normal((40, 64)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    y0 = (rng.standard_normal((4, 100)).astype(np.float32).view(np.uint32) >> 16).astype(np.uint16)
+    sel = np.array([3, 0, 7, 9, 11, 20, 31, 39, 50, 60, 77, 80, 90, 95, 97, 99, 1, 2, 4, 5, 6, 8, 10, 12,
+                    13, 14, 15, 16, 17, 18, 19, 21, 22, 23, 24, 25, 26, 27, 28, 29])
+    view = y0[:, sel]
+    assert not view.flags["C_CONTIGUOUS"] or view.flags["F_CONTIGUOUS"]
+    assert np.array_equal(orc.gemm(x, w, orc.OUT_RESIDUAL, view),
+                          orc.gemm(x, w, orc.OUT_RESIDUAL, np.ascontiguousarray(view)))
+    assert np.array_equal(orc.moe_out(x, x[0], x, x, view[:, :64].T.copy().T),
+                          orc.moe_out(x, x[0], x, x, np.ascontiguousarray(view[:, :64])))
