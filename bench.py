@@ -32,6 +32,11 @@ The kernel-trace summary in profiles/ comes from
     rocprofv3 --kernel-trace --stats -d P -o bench --output-format csv -- python3 bench.py --steps 20 > B
     python3 bench.py --trace-summary P/bench_kernel_trace.csv B '<that rocprofv3 command>'
 
+The clock and matrix-core summary in profiles/ comes from
+
+    rocprofv3 --pmc GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA -d C -o run --output-format csv -- python3 bench.py --traffic-run > T
+    python3 bench.py --clock-summary C/run_counter_collection.csv T '<that rocprofv3 command>'
+
 --traffic-run selects the step's kernels (every candidate is dispatched, so
 every candidate gets counters) and copies COPY_BYTES device to device; the
 summary scales each kernel's FETCH_SIZE and WRITE_SIZE (KiB per dispatch)
@@ -192,6 +197,7 @@ def main():
     ap.add_argument("--traffic-run", action="store_true")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     ap.add_argument("--trace-summary", nargs=3, metavar=("TRACE_CSV", "BENCH_OUT", "COMMAND"))
+    ap.add_argument("--clock-summary", nargs=3, metavar=("COUNTER_CSV", "TRAFFIC_RUN_OUT", "COMMAND"))
     ap.add_argument("--yardstick", action="store_true",
                     help="time hipBLASLt (torch.matmul) on the step's shapes instead")
     args = ap.parse_args()
@@ -200,6 +206,9 @@ def main():
         return
     if args.trace_summary:
         trace_summary(*args.trace_summary)
+        return
+    if args.clock_summary:
+        clock_summary(*args.clock_summary)
         return
     if args.yardstick:
         yardstick(args.steps)
@@ -465,6 +474,60 @@ def traffic_summary(fetch_csv, write_csv):
     with open(path, "w") as fh:
         json.dump(out, fh, indent=1, sort_keys=True)
     print("wrote %s: %d kernels, fetch scale %.4f, write scale %.4f" % (path, len(out) - 1, sf, sw))
+
+
+def clock_summary(counter_csv, picked_json, cmd):
+    """profiles/: the step's GEMMs under `rocprofv3 --pmc GRBM_GUI_ACTIVE
+    SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA` of a --traffic-run: per kernel
+    (its full-block dispatches), the clock it ran at (GRBM_GUI_ACTIVE, summed
+    over the 8 XCDs, / 8 / the dispatch's duration), the matrix cores' busy
+    fraction at that clock (SQ_VALU_MFMA_BUSY_CYCLES / (256 CUs x 4 SIMDs x
+    cycles)), and the TFLOP/s of that dispatch against 2.5 PFLOP/s and
+    against the peak at the clock it ran at."""
+    import csv
+    import statistics
+    picked = None
+    for line in open(picked_json):
+        line = line.strip()
+        if line.startswith("{") and "picked" in line:
+            picked = json.loads(line)["picked"]
+    if not picked:
+        sys.exit("clock summary: no picked-kernels line in %s" % picked_json)
+    per = {}
+    for r in csv.DictReader(open(counter_csv)):
+        key = (r["Kernel_Name"], r["Dispatch_Id"])
+        d = per.setdefault(key, {"grid": int(r["Grid_Size"]),
+                                 "us": (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3})
+        d[r["Counter_Name"]] = float(r["Counter_Value"])
+    shapes = {nm: (k, n) for nm, k, n, _ in LAYER}
+    lines = ["command: " + cmd,
+             "summary: python3 bench.py --clock-summary <the run's counter_collection.csv> <its stdout> '<command>'",
+             "",
+             "The step's GEMMs (BASELINE configs[1], M=%d), dispatches of the full block, medians:" % M]
+    for nm, kern in picked.items():
+        ds = [d for (kn, _), d in per.items() if kn == kern]
+        if not ds:
+            continue
+        top = max(d["grid"] for d in ds)
+        ds = [d for d in ds if d["grid"] == top and "GRBM_GUI_ACTIVE" in d]
+        us = statistics.median(d["us"] for d in ds)
+        clk = statistics.median(d["GRBM_GUI_ACTIVE"] / 8 / d["us"] / 1e3 for d in ds)
+        busy = statistics.median(d["SQ_VALU_MFMA_BUSY_CYCLES"] / (256 * 4 * d["GRBM_GUI_ACTIVE"] / 8) for d in ds)
+        k, n = shapes[nm]
+        tf = 2.0 * M * n * k / us / 1e6
+        lines.append("  %-8s %s" % (nm, kern))
+        lines.append("           %7.2f us  %7.1f TFLOP/s  %.3f of 2.5 PFLOP/s | clock %.2f GHz -> peak %.0f TFLOP/s, "
+                     "%.3f of it | MFMA busy %.3f of the cycles (%d dispatches)" % (
+                         us, tf, tf / MFMA_BF16_PEAK, clk, MFMA_BF16_PEAK * clk / 2.4, tf / (MFMA_BF16_PEAK * clk / 2.4),
+                         busy, len(ds)))
+    lines.append("")
+    lines.append("2.5 PFLOP/s is the dense bf16 peak at 2.4 GHz; the clock each kernel ran at is what the chip's "
+                 "power management gave it (counters collected with the dispatches serialised, so the durations "
+                 "can differ from the bench's back-to-back ones).")
+    path = os.path.join(ROOT, "profiles", "gemm_clock_mfma_layer4b_m2048.txt")
+    with open(path, "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    print("wrote " + path)
 
 
 def bench_moe(g, e, hb):

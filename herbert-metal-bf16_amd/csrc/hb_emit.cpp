@@ -223,9 +223,9 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
             if (d.mv_waves != 4 && d.xsrc == HB_XSRC_NORM)
                 return fail(HB_ERR_UNSUPPORTED, "matvec XSrc::Norm: 4 waves");
             if (d.x_lds > 1 ||
-                (d.x_lds && (mma || (uint64_t)d.mv_m * d.k * 2 > (d.mv_waves == 4 ? 65536u : 147456u))))
+                (d.x_lds && (d.form == 1 || (uint64_t)d.mv_m * d.k * 2 > (d.mv_waves == 4 ? 65536u : 147456u))))
                 return fail(HB_ERR_UNSUPPORTED,
-                            "matvec x_lds: VALU forms, m*k*2 <= 64 KiB of LDS (144 KiB with 8 or 16 waves)");
+                            "matvec x_lds: VALU forms and form 3, m*k*2 <= 64 KiB of LDS (144 KiB with 8 or 16 waves)");
             const bool xl = d.x_lds && d.xsrc != HB_XSRC_NORM;
             if (!d.k || !d.n || d.k % (8 * d.split) || !d.split || (d.split & (d.split - 1)) ||
                 d.split > d.mv_waves)

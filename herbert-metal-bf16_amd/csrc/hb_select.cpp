@@ -926,8 +926,16 @@ std::vector<std::pair<std::string, hb_desc>> mv_candidates(hb_engine* e, uint32_
                     F{8, 4, 0, 16}, F{8, 4, 512, 16}, F{4, 4, 0, 32}, F{4, 4, 512, 32}}) {
             hb_desc d3 = desc(3, f.rows, f.split, f.persist);
             d3.unroll = f.unroll;
-            v.emplace_back("mfl" + std::string(f.rows == 32 ? "_r32" : "") + "_u" + std::to_string(f.unroll) + "k" +
-                    std::to_string(f.split) + (f.persist ? "p" + std::to_string(f.persist) : ""), d3);
+            const std::string nm = "mfl" + std::string(f.rows == 32 ? "_r32" : "") + "_u" + std::to_string(f.unroll) +
+                                   "k" + std::to_string(f.split) + (f.persist ? "p" + std::to_string(f.persist) : "");
+            v.emplace_back(nm, d3);
+            // x (the B operand) staged in LDS once per workgroup: its loads
+            // were a fifth of the form's time, one per row block.
+            if ((uint64_t)mv_m * (k + 8) * 2 + 4ull * (f.rows / 16) * 16 * f.unroll * 16 * 4 <= 160 * 1024 &&
+                (uint64_t)mv_m * k * 2 <= 65536) {
+                d3.x_lds = 1;
+                v.emplace_back(nm + "xl", d3);
+            }
         }
     }
     for (uint32_t split : splits)

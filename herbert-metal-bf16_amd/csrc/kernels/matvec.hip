@@ -30,7 +30,8 @@
 //  3 (MFMA, W through LDS): form 1's MFMAs and x, with W loaded in row
 //    order (512 B or 1 KB of one row per load instruction, as the VALU
 //    forms read it) and turned into the A operand through a wave-private
-//    LDS tile: the MFMA's arithmetic with the VALU forms' HBM access.
+//    LDS tile: the MFMA's arithmetic with the VALU forms' HBM access; its
+//    x (the B operand) from memory, or staged in LDS once per workgroup.
 // Both: SPLIT wavefronts of a workgroup share a row block's K (contiguous
 // ranges); their partials are added in wave order through LDS.  PERSIST
 // > 0: that many workgroups loop over the row blocks.
@@ -95,8 +96,12 @@ constexpr u32 KS = K / SPLIT;                 // K of one wave's range
 static_assert(!SWO || (RB % 2 == 0 && N % 2 == 0 && !HB_MMA), "Out::Swiglu: VALU forms, even rows");
 static_assert(HB_XSRC == 0 || !HB_MMA, "XSrc fusions: VALU forms");
 static_assert(HB_XSRC != 2 || WAVES == 4, "XSrc::Norm: 4 waves");
-static_assert(!HB_XIN_LDS || (!HB_MMA && MV * K * 2 <= (WAVES == 4 ? 65536u : 147456u)),
-              "x in LDS: VALU forms, m*K*2 <= 64 KiB (144 KiB with 8 or 16 waves)");
+static_assert(!HB_XIN_LDS || (HB_FORM != 1 && MV * K * 2 <= (WAVES == 4 ? 65536u : 147456u)),
+              "x in LDS: VALU forms and form 3, m*K*2 <= 64 KiB (144 KiB with 8 or 16 waves)");
+// x rows in LDS, in 16-byte chunks: form 3 reads the B operand of 16 lanes
+// (x rows 0..15) at one K offset, so its rows are one chunk longer (each row
+// four banks on from the last: no conflicts); the VALU forms read one row.
+constexpr u32 XST = HB_FORM == 3 ? K / 8 + 1 : K / 8;
 
 static_assert(WAVES % SPLIT == 0, "split divides the waves");
 static_assert(K % (8 * SPLIT) == 0 && KS % 8 == 0, "K split in whole chunks");
@@ -166,7 +171,7 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
     const u32 gi = wave / SPLIT, sp = wave % SPLIT;  // row block in the group, K part
     const u32 m = m_launch < MV ? m_launch : MV;
 #if HB_XIN_LDS
-    __shared__ u32x4 xn4[MV * K / 8];
+    __shared__ u32x4 xn4[MV * XST];
 #endif
 #if HB_XSRC == 2
     // XSrc::Norm (kernels.rs:355-440, rmsnorm :48-103): each x row's RMSNorm
@@ -230,7 +235,7 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
     auto prologue = [&]() HB_INLINE2 {
         for (u32 c = tid; c < MV * K / 8; c += NT) {
             const u32 j = c / (K / 8), jj = j < m ? j : m - 1;
-            xn4[c] = xmem(jj, (c % (K / 8)) * 8);
+            xn4[j * XST + c % (K / 8)] = xmem(jj, (c % (K / 8)) * 8);
         }
         __syncthreads();
     };
@@ -240,15 +245,18 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
     // after the first W block's loads are issued, whose HBM latency then
     // covers it; otherwise first (measured: hoisting the short staging of
     // plain x, or a prologue a persistent workgroup amortises, lost 1-15%).
-    // The MFMA form reads x from memory.
+    // Form 1 reads x from memory; form 3 from memory, or with HB_XLDS from
+    // LDS (the B operand: one x load per workgroup instead of one per row
+    // block).
     constexpr bool HOIST = HB_XSRC == 2 && HB_PERSIST == 0;
     bool pending = HB_XIN_LDS && !HB_MMA && HOIST;
+    (void)pending;
 #if HB_XIN_LDS
     if constexpr (!HOIST) prologue();
 #endif
     auto xload = [&](u32 jj, u32 off) HB_INLINE2 -> u32x4 {
 #if HB_XIN_LDS
-        return xn4[(jj * K + off) / 8];
+        return xn4[jj * XST + off / 8];
 #else
         return xmem(jj, off);
 #endif
@@ -396,6 +404,16 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
         const u32 fr = lane & 15u, fq = lane >> 4;
         const bool xon = fr < m;
         const u16* xrow = x + (u64)(xon ? fr : 0) * K + k0;
+        // The B operand's 8 bf16 of x row fr at element k0 + off (zeros for
+        // rows past m): from memory, or (form 3 with x in LDS) from LDS.
+        auto xfrag = [&](u32 off) HB_INLINE2 -> u32x4 {
+            if (!xon) return u32x4{0u, 0u, 0u, 0u};
+#if HB_XIN_LDS
+            return xn4[fr * XST + (k0 + off) / 8];
+#else
+            return *(const u32x4*)(xrow + off);
+#endif
+        };
         const u16* wrow[T];  // the A operand's row (fr) of each tile
 #pragma unroll
         for (u32 t = 0; t < T; t++) {
@@ -446,7 +464,7 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
             u32x4 xv[U];
 #pragma unroll
             for (u32 u = 0; u < U; u++)
-                xv[u] = xon ? *(const u32x4*)(xrow + at + (u * 4 + fq) * 8) : u32x4{0u, 0u, 0u, 0u};
+                xv[u] = xfrag(at + (u * 4 + fq) * 8);
 #pragma unroll
             for (u32 u = 0; u < U; u++)
 #pragma unroll
@@ -479,7 +497,7 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
                 wv[u] = __builtin_nontemporal_load((const u32x4*)(wrow[0] + kk + (u * 4 + fq) * 8));
 #pragma unroll
             for (u32 u = 0; u < U; u++)
-                xv[u] = xon ? *(const u32x4*)(xrow + kk + (u * 4 + fq) * 8) : u32x4{0u, 0u, 0u, 0u};
+                xv[u] = xfrag(kk + (u * 4 + fq) * 8);
 #pragma unroll
             for (u32 u = 0; u < U; u++)
                 acc[0][u % NA] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wv[u]),
@@ -488,7 +506,7 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
         }
 #endif
         for (; kk < KS; kk += 32) {
-            const u32x4 xv = xon ? *(const u32x4*)(xrow + kk + fq * 8) : u32x4{0u, 0u, 0u, 0u};
+            const u32x4 xv = xfrag(kk + fq * 8);
 #pragma unroll
             for (u32 t = 0; t < T; t++) {
                 const u32x4 wv = *(const u32x4*)(wrow[t] + kk + fq * 8);

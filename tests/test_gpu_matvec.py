@@ -239,6 +239,28 @@ def test_matvec_x_in_lds(gpu, name, k, n, out, form, m):
     check_close(got, want, k, abs_products(x, w), "%s %s xl m=%d" % (name, form, m), acc=acc)
 
 
+MFL_XL_FORMS = {"mfl_u4_k4": dict(form=3, split=4, unroll=4),
+                "mfl_r32_u4_k4_p512": dict(form=3, rows=32, split=4, unroll=4, persist=512),
+                "mfl_u8_k2": dict(form=3, split=2, unroll=8)}
+
+
+@pytest.mark.parametrize("m", [1, 3, 8])
+@pytest.mark.parametrize("form", sorted(MFL_XL_FORMS))
+@pytest.mark.parametrize("name,k,n,out", SHAPES[:3])
+def test_matvec_mfl_x_in_lds(gpu, name, k, n, out, form, m):
+    """Form 3 with its B operand (x) staged in LDS once per workgroup, rows
+    one chunk apart: bit-equal to the same form reading x from memory, and
+    within the contract of the oracle; m=3 on a kernel built for 8 rows."""
+    x = hb.normal_bf16(0x5EED0025, 1.0, (m, k))
+    w = hb.normal_bf16(0x5EED0026, 0.02, (n, k))
+    y0 = hb.normal_bf16(21, 1.0, (m, n)) if out == 2 else None
+    got = run_mv(gpu, x, w, out, y0, x_lds=True, **MFL_XL_FORMS[form])
+    ref = run_mv(gpu, x, w, out, y0, **MFL_XL_FORMS[form])
+    assert np.array_equal(got, ref), "%s %s m=%d: form 3 with x in LDS differs" % (name, form, m)
+    acc = orc.gemm(x, w, orc.OUT_F32) if out == 2 else None
+    check_close(got, orc.gemm(x, w, out, y0), k, abs_products(x, w), "%s %s m=%d" % (name, form, m), acc=acc)
+
+
 WAVE_FORMS = {"w16_r1_p256_u4": dict(waves=16, rows=1, persist=256, unroll=4),
               "w16_r1_u8": dict(waves=16, rows=1, unroll=8),
               "w8_r2_p256_u4": dict(waves=8, rows=2, persist=256, unroll=4)}
