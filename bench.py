@@ -32,11 +32,6 @@ The kernel-trace summary in profiles/ comes from
     rocprofv3 --kernel-trace --stats -d P -o bench --output-format csv -- python3 bench.py --steps 20 > B
     python3 bench.py --trace-summary P/bench_kernel_trace.csv B '<that rocprofv3 command>'
 
-The clock and matrix-core summary in profiles/ comes from
-
-    rocprofv3 --pmc GRBM_GUI_ACTIVE SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA -d C -o run --output-format csv -- python3 bench.py --traffic-run > T
-    python3 bench.py --clock-summary C/run_counter_collection.csv T '<that rocprofv3 command>'
-
 --traffic-run selects the step's kernels (every candidate is dispatched, so
 every candidate gets counters) and copies COPY_BYTES device to device; the
 summary scales each kernel's FETCH_SIZE and WRITE_SIZE (KiB per dispatch)
@@ -197,7 +192,6 @@ def main():
     ap.add_argument("--traffic-run", action="store_true")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     ap.add_argument("--trace-summary", nargs=3, metavar=("TRACE_CSV", "BENCH_OUT", "COMMAND"))
-    ap.add_argument("--clock-summary", nargs=3, metavar=("COUNTER_CSV", "TRAFFIC_RUN_OUT", "COMMAND"))
     ap.add_argument("--yardstick", action="store_true",
                     help="time hipBLASLt (torch.matmul) on the step's shapes instead")
     args = ap.parse_args()
@@ -206,9 +200,6 @@ def main():
         return
     if args.trace_summary:
         trace_summary(*args.trace_summary)
-        return
-    if args.clock_summary:
-        clock_summary(*args.clock_summary)
         return
     if args.yardstick:
         yardstick(args.steps)
@@ -238,7 +229,7 @@ def main():
         per_gemm[name] = {"kernel": g.kernel_name(kern), "flops": f, "op": op}
     log("[bench] selection done in %.1f s" % (time.time() - t0))
     if args.traffic_run:
-        traffic_run(g, ops, per_gemm)
+        traffic_run(g, e, ops, per_gemm)
         return
 
     # Warmup, then exactly K steps between two synchronisations (events at
@@ -263,11 +254,9 @@ def main():
     roofline = {"bound": "mfma", "achieved": round(dd["tflops"], 1), "peak": MFMA_BF16_PEAK,
                 "unit": "TFLOP/s", "frac": round(dd["tflops"] / MFMA_BF16_PEAK, 4), "traffic": None,
                 "kernel": dd["kernel"], "gemm": dom, "launch_us": round(dd["us"], 2)}
-    traffic_file = os.path.join(ROOT, "profiles", "traffic.json")
-    if os.path.exists(traffic_file):
-        tr = json.load(open(traffic_file)).get(dd["kernel"])
-        if tr:
-            roofline["traffic"] = tr["bytes"]
+    tr = traffic_of(dd["kernel"])
+    if tr:
+        roofline["traffic"] = tr["bytes"]
 
     result = {
         "metric": "bf16 GEMM TFLOP/s + % MFMA peak (M=2048); decode matvec HBM GB/s + % peak",
@@ -300,6 +289,15 @@ def main():
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_rows)
     print(json.dumps(result), flush=True)
+
+
+def traffic_of(kernel):
+    """The kernel's HBM bytes per launch from profiles/traffic.json (FETCH_SIZE
+    + WRITE_SIZE of its full-block dispatches, scaled), or None."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if not os.path.exists(path):
+        return None
+    return json.load(open(path)).get(kernel)
 
 
 def gemm_set(g, e, hb, shapes, m, steps, seed):
@@ -336,17 +334,28 @@ def bench_prefill_more(g, e, hb, steps):
     config 4 (27B-class shapes at M=2048, lm_head included)."""
     steps = max(3, min(steps, 10))
     res = {"config1": gemm_set(g, e, hb, CONFIG1, 512, steps, 0x5EED0001)}
+    # config 1's kernel name is its own (no other case has 1024 x 3584), so
+    # its traffic counters are config 1's: HBM bytes per launch against the
+    # algorithmic 2*(M*K + N*K + M*N).
+    c1 = res["config1"]["gemms"]["gemm"]
+    tr = traffic_of(c1["kernel"])
+    k, n = CONFIG1[0][1], CONFIG1[0][2]
+    c1["algorithmic_bytes"] = 2 * (512 * k + n * k + 512 * n)
+    c1["traffic"] = tr["bytes"] if tr else None
     for m in (512, 1024):
         res["config2_m%d" % m] = gemm_set(g, e, hb, LAYER, m, steps, SEED)
     res["config4_m2048"] = gemm_set(g, e, hb, CONFIG4, M, steps, 0x5EED0004)
     return res
 
 
-def traffic_run(g, ops, per_gemm):
-    """The picked kernels a few times, then the calibration copy (a device
-    to device copy of COPY_BYTES, HIP's blit kernel)."""
+def traffic_run(g, e, ops, per_gemm):
+    """The picked kernels a few times, config 1's GEMM (its selection and
+    pick), then the calibration copy (a device to device copy of
+    COPY_BYTES, HIP's blit kernel)."""
     import herbert_hip as hb
     g.time_ops(ops, 3)
+    g.sync()
+    c1 = gemm_set(g, e, hb, CONFIG1, 512, 3, 0x5EED0001)
     g.sync()
     a, b = g.alloc(COPY_BYTES), g.alloc(COPY_BYTES)
     g.zero(a)
@@ -356,7 +365,7 @@ def traffic_run(g, ops, per_gemm):
     g.free(a)
     g.free(b)
     print(json.dumps({"picked": {nm: d["kernel"] for nm, d in per_gemm.items()},
-                      "copy_bytes": COPY_BYTES}), flush=True)
+                      "config1": c1["gemms"]["gemm"]["kernel"], "copy_bytes": COPY_BYTES}), flush=True)
 
 
 def trace_summary(trace_csv, bench_json, cmd):
@@ -369,6 +378,15 @@ def trace_summary(trace_csv, bench_json, cmd):
     import statistics
     b = json.loads([ln for ln in open(bench_json) if ln.startswith("{")][-1])
     rows = sorted(csv.DictReader(open(trace_csv)), key=lambda r: int(r["Start_Timestamp"]))
+    # A split-K GEMM (name "..._ks<s>") is two dispatches, the parts and
+    # their reduce: one launch from the first's start to the second's end.
+    merged = []
+    for r in rows:
+        if r["Kernel_Name"].startswith("gemm_splitk_") and merged and "_ks" in merged[-1]["Kernel_Name"]:
+            merged[-1] = dict(merged[-1], End_Timestamp=r["End_Timestamp"])
+        else:
+            merged.append(r)
+    rows = merged
 
     def dur(r):
         return (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
@@ -407,6 +425,23 @@ def trace_summary(trace_csv, bench_json, cmd):
         d2 = [dur(r) for r in last if r["Kernel_Name"] == nm]
         out.append("  %-8s %-66s rocprof avg %7.2f us (step region) %7.2f us (event region) | bench event "
                    "avg %7.2f us" % (g, nm, statistics.mean(d1), statistics.mean(d2), b["config"]["gemms"][g]["us"]))
+    pm = b.get("prefill_more")
+    if pm:
+        out += ["", "other prefill cases (bench per-launch event times; rocprof average of the kernel's last 40 "
+                    "dispatches, a split-K GEMM with its reduce):"]
+        uses = {}
+        for st in list(pm.values()) + [b["config"]]:
+            for d in st["gemms"].values():
+                uses[d["kernel"]] = uses.get(d["kernel"], 0) + 1
+        for case, st in pm.items():
+            out.append("  %s: %.1f TFLOP/s (%.1f%% of 2.5 PFLOP/s), %.2f us a set" % (
+                case, st["tflops"], 100 * st["frac"], st["us"]))
+            for g, d in st["gemms"].items():
+                if uses[d["kernel"]] > 1:
+                    rp = "rocprof: n/a (the kernel serves another M too)"
+                else:
+                    rp = "rocprof avg %7.2f us" % avg_of(d["kernel"])[1]
+                out.append("    %-8s %-70s bench %7.2f us | %s" % (g, d["kernel"], d["us"], rp))
     mv = b.get("matvec")
     if mv:
         out += ["", "decode (M=1) kernels, rocprof average of their last 40 dispatches:"]
@@ -474,60 +509,6 @@ def traffic_summary(fetch_csv, write_csv):
     with open(path, "w") as fh:
         json.dump(out, fh, indent=1, sort_keys=True)
     print("wrote %s: %d kernels, fetch scale %.4f, write scale %.4f" % (path, len(out) - 1, sf, sw))
-
-
-def clock_summary(counter_csv, picked_json, cmd):
-    """profiles/: the step's GEMMs under `rocprofv3 --pmc GRBM_GUI_ACTIVE
-    SQ_VALU_MFMA_BUSY_CYCLES SQ_INSTS_MFMA` of a --traffic-run: per kernel
-    (its full-block dispatches), the clock it ran at (GRBM_GUI_ACTIVE, summed
-    over the 8 XCDs, / 8 / the dispatch's duration), the matrix cores' busy
-    fraction at that clock (SQ_VALU_MFMA_BUSY_CYCLES / (256 CUs x 4 SIMDs x
-    cycles)), and the TFLOP/s of that dispatch against 2.5 PFLOP/s and
-    against the peak at the clock it ran at."""
-    import csv
-    import statistics
-    picked = None
-    for line in open(picked_json):
-        line = line.strip()
-        if line.startswith("{") and "picked" in line:
-            picked = json.loads(line)["picked"]
-    if not picked:
-        sys.exit("clock summary: no picked-kernels line in %s" % picked_json)
-    per = {}
-    for r in csv.DictReader(open(counter_csv)):
-        key = (r["Kernel_Name"], r["Dispatch_Id"])
-        d = per.setdefault(key, {"grid": int(r["Grid_Size"]),
-                                 "us": (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3})
-        d[r["Counter_Name"]] = float(r["Counter_Value"])
-    shapes = {nm: (k, n) for nm, k, n, _ in LAYER}
-    lines = ["command: " + cmd,
-             "summary: python3 bench.py --clock-summary <the run's counter_collection.csv> <its stdout> '<command>'",
-             "",
-             "The step's GEMMs (BASELINE configs[1], M=%d), dispatches of the full block, medians:" % M]
-    for nm, kern in picked.items():
-        ds = [d for (kn, _), d in per.items() if kn == kern]
-        if not ds:
-            continue
-        top = max(d["grid"] for d in ds)
-        ds = [d for d in ds if d["grid"] == top and "GRBM_GUI_ACTIVE" in d]
-        us = statistics.median(d["us"] for d in ds)
-        clk = statistics.median(d["GRBM_GUI_ACTIVE"] / 8 / d["us"] / 1e3 for d in ds)
-        busy = statistics.median(d["SQ_VALU_MFMA_BUSY_CYCLES"] / (256 * 4 * d["GRBM_GUI_ACTIVE"] / 8) for d in ds)
-        k, n = shapes[nm]
-        tf = 2.0 * M * n * k / us / 1e6
-        lines.append("  %-8s %s" % (nm, kern))
-        lines.append("           %7.2f us  %7.1f TFLOP/s  %.3f of 2.5 PFLOP/s | clock %.2f GHz -> peak %.0f TFLOP/s, "
-                     "%.3f of it | MFMA busy %.3f of the cycles (%d dispatches)" % (
-                         us, tf, tf / MFMA_BF16_PEAK, clk, MFMA_BF16_PEAK * clk / 2.4, tf / (MFMA_BF16_PEAK * clk / 2.4),
-                         busy, len(ds)))
-    lines.append("")
-    lines.append("2.5 PFLOP/s is the dense bf16 peak at 2.4 GHz; the clock each kernel ran at is what the chip's "
-                 "power management gave it (counters collected with the dispatches serialised, so the durations "
-                 "can differ from the bench's back-to-back ones).")
-    path = os.path.join(ROOT, "profiles", "gemm_clock_mfma_layer4b_m2048.txt")
-    with open(path, "w") as fh:
-        fh.write("\n".join(lines) + "\n")
-    print("wrote " + path)
 
 
 def bench_moe(g, e, hb):
