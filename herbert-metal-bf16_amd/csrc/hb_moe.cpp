@@ -18,6 +18,11 @@ int moe_experts_run(hb_gpu* g, const int32_t kernels[4], int32_t swiglu, int32_t
         return fail(HB_ERR_INVALID, "moe experts: a kernel of the layer is not built");
     if (sd->kind != HB_KIND_SORT && sd->kind != HB_KIND_SORT_ATOMIC)
         return fail(HB_ERR_INVALID, "moe experts: kernels[0] is not a moe_sort");
+    // Grouped expert GEMMs only (never a dense split-K pair, whose
+    // workspace the static entry point could not allocate).
+    if (gd->rows_of == HB_ROWS_DENSE || kernel_desc(g, dn)->rows_of == HB_ROWS_DENSE ||
+        kernel_desc(g, dn)->kind != HB_KIND_GEMM)
+        return fail(HB_ERR_INVALID, "moe experts: kernels[1] and kernels[2] are grouped expert GEMMs");
     const bool fused = gd->kind == HB_KIND_GEMM_SWIGLU;
     if (!fused && !kernel_desc(g, swiglu))
         return fail(HB_ERR_INVALID, "moe experts: the gate|up GEMM needs the swiglu_slots kernel");

@@ -58,7 +58,8 @@ extern "C" int hb_moe_experts_run_static(hb_gpu* g, const int32_t kernels[4], in
     const hb_desc* sd = kernel_desc(g, kernels[0]);
     const hb_desc* gd = kernel_desc(g, kernels[1]);
     const hb_desc* dd = kernel_desc(g, kernels[2]);
-    if (!sd || !gd || !dd || (sd->kind != HB_KIND_SORT && sd->kind != HB_KIND_SORT_ATOMIC))
+    if (!sd || !gd || !dd || (sd->kind != HB_KIND_SORT && sd->kind != HB_KIND_SORT_ATOMIC) ||
+        gd->rows_of == HB_ROWS_DENSE || dd->rows_of == HB_ROWS_DENSE)
         return fail(HB_ERR_INVALID, "moe experts (static): kernels[0..2] must be a built sort and grouped GEMMs");
     if (m == 0) return fail(HB_ERR_INVALID, "moe experts (static): 0 rows");
     const bool fused = gd->kind == HB_KIND_GEMM_SWIGLU, gather = kernels[3] >= 0;

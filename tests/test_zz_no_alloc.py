@@ -77,3 +77,32 @@ def test_static_refuses_blocks_beyond_the_array(gpu):
         layer.free()
         for buf in (Wgu, Wdn, out):
             gpu.free(buf)
+
+
+def test_static_refuses_a_dense_kernel_for_the_experts(gpu):
+    """A dense GEMM (here a split-K pair, whose workspace the context would
+    have to allocate) passed where a grouped expert GEMM belongs: refused
+    before anything is launched or allocated."""
+    E, K, H, MI, rows = 64, 4, 1024, 256, 64
+    Wgu, Wdn = gpu.alloc(E * 2 * MI * H * 2), gpu.alloc(E * H * MI * 2)
+    gpu.zero(Wgu)
+    gpu.zero(Wdn)
+    out = gpu.alloc(rows * H * 2)
+    with hb.Engine(gpu, "") as e:
+        layer = hb.MoeLayer(gpu, e, E, K, H, MI, rows, Wgu, Wdn,
+                            scores=hb.normal_bf16(7, 1.0, (rows, E)), x=hb.normal_bf16(8, 1.0, (rows, H)))
+    try:
+        dense = gpu.pipeline(hb.gemm_mma(H, 2 * MI, 0, bm=128, bn=128, bk=64, wm=2, wn=2, mfma=16, dbuf=1,
+                                         lds_dma=1, order=1, ksplit=2))
+        good = list(layer.kernels)
+        for slot in (1, 2):
+            layer.kernels = list(good)
+            layer.kernels[slot] = dense
+            rc = run_static(gpu, layer, out, rows)
+            assert rc == hb.ERR_INVALID, slot
+            assert "grouped" in hb.last_error()
+        layer.kernels = good
+    finally:
+        layer.free()
+        for buf in (Wgu, Wdn, out):
+            gpu.free(buf)
