@@ -276,6 +276,8 @@ const Form kMoreForms[] = {
     // (hb_desc.sched 1), four stages of 32 K: 256 x 288 tiles fill exactly
     // two rounds of the CUs on 2048 x 18432 (and 4608: 128 tiles).
     {"pp_t256x288", 256, 288, 32, 4, 2, 16, 3, 1, 1, 0, 1},
+    {"pp_t256x288_b4", 256, 288, 32, 4, 2, 16, 3, 1, 1, 4, 1},
+    {"pp_t256x256_b4", 256, 256, 32, 4, 2, 16, 3, 1, 1, 4, 1},
     {"pp_t256x256", 256, 256, 32, 4, 2, 16, 3, 1, 1, 0, 1},
     {"pp_t256x192", 256, 192, 32, 4, 2, 16, 3, 1, 1, 0, 1},
     {"pp_t256x128", 256, 128, 32, 4, 2, 16, 3, 1, 1, 0, 1},
@@ -285,6 +287,8 @@ const Form kMoreForms[] = {
     // 4608 (232 tiles), 128 x 160 on 2048 x 2560 (256), three or four
     // stages of 64 K (longer MFMA phases than 32 K at these wave tiles).
     {"pp_t256x160_k64", 256, 160, 64, 4, 2, 16, 2, 1, 1, 0, 1},
+    {"pp_t256x160_k64_b2", 256, 160, 64, 4, 2, 16, 2, 1, 1, 2, 1},
+    {"pp_t256x160_k64_b4", 256, 160, 64, 4, 2, 16, 2, 1, 1, 4, 1},
     {"pp_t128x160_k64", 128, 160, 64, 4, 2, 16, 3, 1, 1, 0, 1},
     {"pp_t128x160_k64_b4", 128, 160, 64, 4, 2, 16, 3, 1, 1, 4, 1},
     {"pp_t128x288_k64", 128, 288, 64, 4, 2, 16, 2, 1, 1, 0, 1},

@@ -37,6 +37,8 @@ TILES = {
     "pp_t256x288": dict(bm=256, bn=288, bk=32, wm=4, wn=2, mfma=16, dbuf=3, lds_dma=1, order=1, sched=1),
     "pp_t256x256_b4": dict(bm=256, bn=256, bk=32, wm=4, wn=2, mfma=16, dbuf=3, lds_dma=1, order=1,
                            band=4, sched=1),
+    "pp_t256x288_b4": dict(bm=256, bn=288, bk=32, wm=4, wn=2, mfma=16, dbuf=3, lds_dma=1, order=1,
+                           band=4, sched=1),
     "pp_t128x128": dict(bm=128, bn=128, bk=32, wm=2, wn=4, mfma=16, dbuf=3, lds_dma=1, order=1, sched=1),
     "pp_t128x256_s3": dict(bm=128, bn=256, bk=32, wm=2, wn=4, mfma=16, dbuf=2, lds_dma=1, order=0,
                            sched=1),
