@@ -14,6 +14,7 @@
 #include <cstring>
 #include <fstream>
 #include <sstream>
+#include <dlfcn.h>
 #include <sys/stat.h>
 #include <unistd.h>
 
@@ -63,12 +64,36 @@ static uint64_t fnv1a(const std::string& s, uint64_t h = 1469598103934665603ull)
     return h;
 }
 
+// The disk cache of compiled kernels: $HB_CACHE_DIR ("" disables it), else
+// _kcache beside this library (build.py fills it for the kernels its
+// manifest lists, so a fresh box finds them compiled), else
+// ~/.cache/herbert_hip when that directory cannot be written.
 static std::string cache_dir() {
     const char* d = getenv("HB_CACHE_DIR");
-    if (d) return d;  // "" disables the disk cache
+    if (d) return d;
+    Dl_info info;
+    if (dladdr((void*)&cache_dir, &info) && info.dli_fname) {
+        std::string lib = info.dli_fname;
+        const size_t slash = lib.rfind('/');
+        const std::string dir = (slash == std::string::npos ? std::string(".") : lib.substr(0, slash)) + "/_kcache";
+        mkdir(dir.c_str(), 0755);
+        if (access(dir.c_str(), W_OK) == 0) return dir;
+    }
     const char* home = getenv("HOME");
     if (!home || !*home) return "";
     return std::string(home) + "/.cache/herbert_hip";
+}
+
+// HB_KERNEL_MANIFEST=path: every kernel a context builds appends its
+// descriptor (the hb_desc fields in order, decimal) to that file, the list
+// build.py precompiles.
+static void manifest_add(const hb_desc& d) {
+    const char* path = getenv("HB_KERNEL_MANIFEST");
+    if (!path || !*path) return;
+    std::ofstream f(path, std::ios::app);
+    const uint32_t* w = (const uint32_t*)&d;
+    for (size_t i = 0; i < sizeof(hb_desc) / 4; i++) f << (i ? " " : "") << w[i];
+    f << "\n";
 }
 
 static void mkdirs(const std::string& p) {
@@ -164,6 +189,7 @@ static int load_kernel(hb_gpu* g, const hb_desc& d, Kernel* k) {
     k->desc = d;
     int rc = emit(d, &k->em);
     if (rc) return rc;
+    manifest_add(d);
     auto t0 = std::chrono::steady_clock::now();
     std::string code;
     rc = compile(k->em, g->arch, &code);
@@ -407,6 +433,24 @@ int hb_zero(hb_gpu* g, hb_buf buf, uint64_t offset, uint64_t bytes) {
         void* args[2] = {&ptr, &n};
         HB_HIP(hipModuleLaunchKernel(g->zero_kernel.fn, (uint32_t)groups, 1, 1, 256, 1, 1, 0,
                                      g->stream, args, nullptr));
+    }
+    return HB_OK;
+}
+
+int hb_kernel_precompile(const hb_desc* desc) {
+    hb_desc d = with_defaults(*desc);
+    Emitted em;
+    int rc = emit(d, &em);
+    if (rc) return rc;
+    std::string code;
+    if ((rc = compile(em, "gfx950", &code))) return rc;
+    if (d.kind == HB_KIND_GEMM && d.ksplit > 1) {
+        hb_desc rd{};
+        rd.kind = KIND_SPLITK_REDUCE;
+        rd.n = d.n;
+        rd.out = d.out;
+        rd.ksplit = d.ksplit;
+        return hb_kernel_precompile(&rd);
     }
     return HB_OK;
 }

@@ -187,6 +187,12 @@ typedef struct hb_desc {
  * constants, cached by name in the context (QwenEngine::get, qwen.rs:1156-1166)
  * and on disk by source hash.  *kernel is the pipeline's index. */
 int hb_kernel_build(hb_gpu *gpu, const hb_desc *desc, int32_t *kernel);
+/* No counterpart in the reference (Metal compiles its MSL at load and keeps
+ * its own pipeline cache): the kernel `desc` names compiled for gfx950 into
+ * the disk cache, with no GPU and no context -- build.py warms the cache for
+ * the kernels a manifest lists, so a fresh box does not spend minutes in
+ * hiprtc at load.  HB_OK, or the error that building it gives. */
+int hb_kernel_precompile(const hb_desc *desc);
 /* Emitted::name: the descriptor in the reference's naming
  * (gemm_mma_{K}x{N}_{bf16|f32|res}..., prefill.rs:1295-1300). */
 const char *hb_kernel_name(hb_gpu *gpu, int32_t kernel);
