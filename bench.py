@@ -61,6 +61,7 @@ CONFIG4 = [("qkv", 5120, 7168, 0), ("gate_up", 5120, 34816, 0), ("down", 17408, 
 DECODE_LAYERS = 4
 SEED = 0x5EED0002  # config 2's seeds: X = SEED + 2i, W = SEED + 2i + 1
 COPY_BYTES = 1 << 28  # the calibration copy of the traffic counters
+MARK_BYTES = 7 * 4096  # the trace marker fill: 7 workgroups of 256 threads
 
 
 def log(*a):
@@ -314,9 +315,16 @@ def gemm_set(g, e, hb, shapes, m, steps, seed):
         kern = e.gemm(k, n, out, hb.r(state), hb.r(W), hb.r(X), hb.r(Y), m)
         ops.append(hb.Op(kern, [hb.r(state), hb.r(W), hb.r(X), hb.r(Y), hb.r(state), hb.r(state)], m))
         flops.append(2.0 * m * n * k)
+    # Trace markers around the timed region (a fill of MARK_BYTES: its
+    # dispatch's grid tells it apart in a kernel trace).
+    mark = g.alloc(MARK_BYTES)
+    bufs.append(mark)
     g.time_ops(ops, 2)
+    g.zero(mark)
     t = g.time_ops(ops, steps)
     _, each = g.time_each(ops, steps)
+    g.zero(mark)
+    g.sync()
     out = {"m": m, "tflops": round(sum(flops) / (t / steps) / 1e12, 1),
            "frac": round(sum(flops) / (t / steps) / 1e12 / MFMA_BF16_PEAK, 4),
            "us": round(t / steps * 1e6, 2), "gemms": {}}
@@ -427,21 +435,23 @@ def trace_summary(trace_csv, bench_json, cmd):
                    "avg %7.2f us" % (g, nm, statistics.mean(d1), statistics.mean(d2), b["config"]["gemms"][g]["us"]))
     pm = b.get("prefill_more")
     if pm:
-        out += ["", "other prefill cases (bench per-launch event times; rocprof average of the kernel's last 40 "
-                    "dispatches, a split-K GEMM with its reduce):"]
-        uses = {}
-        for st in list(pm.values()) + [b["config"]]:
-            for d in st["gemms"].values():
-                uses[d["kernel"]] = uses.get(d["kernel"], 0) + 1
-        for case, st in pm.items():
-            out.append("  %s: %.1f TFLOP/s (%.1f%% of 2.5 PFLOP/s), %.2f us a set" % (
-                case, st["tflops"], 100 * st["frac"], st["us"]))
+        out += ["", "other prefill cases (bench per-launch event times; rocprof averages over the set's timed "
+                    "region, a split-K GEMM with its reduce):"]
+        # Each set's timed region lies between two marker fills (grid of
+        # MARK_BYTES / 16 threads), the sets in the bench's order.
+        marks = [i for i, r in enumerate(rows) if r["Kernel_Name"] == "fill_zero"
+                 and int(r.get("Grid_Size_X", r.get("Grid_Size", 0))) == MARK_BYTES // 16]
+        regions = [rows[marks[2 * i] + 1:marks[2 * i + 1]] for i in range(len(marks) // 2)]
+        for ci, (case, st) in enumerate(pm.items()):
+            reg = regions[ci] if ci < len(regions) else []
+            out.append("  %s: %.1f TFLOP/s (%.1f%% of 2.5 PFLOP/s), %.2f us a set; rocprof first-start..last-end "
+                       "%.2f us a set" % (case, st["tflops"], 100 * st["frac"], st["us"],
+                                          (int(reg[-1]["End_Timestamp"]) - int(reg[0]["Start_Timestamp"])) / 1e3
+                                          / (len(reg) / len(st["gemms"])) if reg else float("nan")))
             for g, d in st["gemms"].items():
-                if uses[d["kernel"]] > 1:
-                    rp = "rocprof: n/a (the kernel serves another M too)"
-                else:
-                    rp = "rocprof avg %7.2f us" % avg_of(d["kernel"])[1]
-                out.append("    %-8s %-70s bench %7.2f us | %s" % (g, d["kernel"], d["us"], rp))
+                dd = [dur(r) for r in reg if r["Kernel_Name"] == d["kernel"]]
+                out.append("    %-8s %-70s bench %7.2f us | rocprof avg %7.2f us (%d in the timed region)" % (
+                    g, d["kernel"], d["us"], statistics.mean(dd) if dd else float("nan"), len(dd)))
     mv = b.get("matvec")
     if mv:
         out += ["", "decode (M=1) kernels, rocprof average of their last 40 dispatches:"]
