@@ -15,6 +15,7 @@
 #include <fstream>
 #include <sstream>
 #include <dlfcn.h>
+#include <utime.h>
 #include <sys/stat.h>
 #include <unistd.h>
 
@@ -117,9 +118,13 @@ static int compile(const Emitted& em, const std::string& arch, std::string* code
                                      "-packed-fp32-ops"};
     for (const auto& d : em.defines) opts.push_back(d);
     opts.push_back("-DHB_NAME=" + em.name);
-    // The disk cache: the source, its headers and the options hashed.
+    // The disk cache: the source, the headers (every embedded .h) and the
+    // options hashed; an edit to another kernel source keeps this entry.
     std::string key = text;
-    for (const auto& s : kSources) key += s.text;
+    for (const auto& s : kSources) {
+        const size_t len = strlen(s.name);
+        if (len > 2 && strcmp(s.name + len - 2, ".h") == 0) key += s.text;
+    }
     for (const auto& o : opts) key += "\n" + o;
     key += "\nhiprtc" + std::to_string(HIP_VERSION);
     char hex[32];
@@ -132,7 +137,10 @@ static int compile(const Emitted& em, const std::string& arch, std::string* code
             std::stringstream b;
             b << f.rdbuf();
             *code = b.str();
-            if (!code->empty()) return HB_OK;
+            if (!code->empty()) {
+                utime(path.c_str(), nullptr);  // in use: build.py keeps entries touched by its warm-up
+                return HB_OK;
+            }
         }
     }
     std::vector<const char*> hnames, htexts;

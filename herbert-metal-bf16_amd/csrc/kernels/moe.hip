@@ -244,11 +244,12 @@ extern "C" __global__ __launch_bounds__(1024) void HB_NAME(const u32* __restrict
             list[pos] = i;
         }
         // The group's first lane advances the wave's cursor after every
-        // lane has read it.
-        __builtin_amdgcn_s_waitcnt(0);
+        // lane has read it: only the LDS accesses are ordered (lgkmcnt 0;
+        // the list stores are not waited for).
+        __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_wave_barrier();
         if (on && lower == 0) hist[w][x] += (u32)__popcll(same);
-        __builtin_amdgcn_s_waitcnt(0);
+        __builtin_amdgcn_s_waitcnt(0xC07F);
         __builtin_amdgcn_wave_barrier();
     };
     if constexpr (HOLD) {
