@@ -171,6 +171,16 @@ def yardstick(steps):
     t = t_of(step, steps)
     fl = sum(2.0 * M * n * k for _, k, n, _, _ in mats)
     lines.append("  step (qkv, o, gate_up, down back to back): %8.2f us %7.1f TFLOP/s" % (t * 1e6, fl / t / 1e12))
+    # config 1 and config 2 at M=512 and 1024, the same seeds as the bench's sets
+    x1 = torch.from_numpy(hb.normal_bf16(0x5EED0001, 1.0, (512, 1024)).view(np.int16)).view(torch.bfloat16).to(dev)
+    w1 = torch.from_numpy(hb.normal_bf16(0x5EED0002, 0.02, (3584, 1024)).view(np.int16)).view(torch.bfloat16).to(dev)
+    t = t_of(lambda: torch.matmul(x1, w1.t()), steps)
+    lines.append("  config 1 (M=512 K=1024 N=3584): %8.2f us %7.1f TFLOP/s" % (t * 1e6, 2.0 * 512 * 1024 * 3584 / t / 1e12))
+    for mm in (512, 1024):
+        sub = [(name, k, n, x[:mm].contiguous(), w) for name, k, n, x, w in mats]
+        t = t_of(lambda: [torch.matmul(x, w.t()) for _, _, _, x, w in sub], steps)
+        fl = sum(2.0 * mm * n * k for _, k, n, _, _ in sub)
+        lines.append("  config 2 at M=%d, the four back to back: %8.2f us %7.1f TFLOP/s" % (mm, t * 1e6, fl / t / 1e12))
     s = 8192
     a = torch.randn(s, s, device=dev, dtype=torch.bfloat16)
     bmat = torch.randn(s, s, device=dev, dtype=torch.bfloat16)
