@@ -32,6 +32,7 @@ TILES = {
     "t256x256_w8_x32_b4": dict(bm=256, bn=256, bk=64, wm=4, wn=2, mfma=32, dbuf=1, lds_dma=1, order=1,
                                band=4),
     "t128x160_s4_b4": dict(bm=128, bn=160, bk=64, wm=2, wn=2, mfma=16, dbuf=3, lds_dma=1, order=1, band=4),
+    "t64x128_s4_w8": dict(bm=64, bn=128, bk=64, wm=2, wn=4, mfma=16, dbuf=3, lds_dma=1, order=1),
     "t32x64_s3": dict(bm=32, bn=64, bk=64, wm=1, wn=4, mfma=16, dbuf=2, lds_dma=1, order=1),
     # the ping-pong schedule (hb_desc.sched 1, 2: two wave groups taking turns)
     "pp_t256x288": dict(bm=256, bn=288, bk=32, wm=4, wn=2, mfma=16, dbuf=3, lds_dma=1, order=1, sched=1),
