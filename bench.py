@@ -72,9 +72,12 @@ MARK_BYTES = 7 * 4096  # the trace marker fill: 7 workgroups of 256 threads
 HEAT_S = 1.0
 
 
-def heat(g, ops, seconds=HEAT_S):
-    """The ops run back to back, ~50 ms a submission, until `seconds` of GPU
-    time have passed (untimed)."""
+def heat(g, ops, seconds=None):
+    """The ops run back to back, ~50 ms a submission, until `seconds` (HEAT_S
+    by default) of GPU time have passed (untimed)."""
+    seconds = HEAT_S if seconds is None else seconds
+    if seconds <= 0:
+        return
     one = g.time_ops(ops, 1)
     reps = int(max(1, min(4096, 0.05 / max(one, 1e-6))))
     total = 0.0
@@ -213,6 +216,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--tune", default="")
+    ap.add_argument("--heat", type=float, default=HEAT_S,
+                    help="seconds of load before each timed region (0: none, the cold-clock figures)")
     ap.add_argument("--cpu-rows", type=int, default=512)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-matvec", action="store_true")
@@ -238,6 +243,8 @@ def main():
               "each GEMM by N across GPUs, which is not built" % args.gpus, file=sys.stderr)
         sys.exit(2)
 
+    global HEAT_S
+    HEAT_S = max(0.0, args.heat)
     import herbert_hip as hb
     g = hb.Gpu(0)
     log("[gpu]", g.summary())
