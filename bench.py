@@ -211,6 +211,7 @@ def yardstick(steps):
 
 
 def main():
+    global HEAT_S
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
@@ -243,7 +244,6 @@ def main():
               "each GEMM by N across GPUs, which is not built" % args.gpus, file=sys.stderr)
         sys.exit(2)
 
-    global HEAT_S
     HEAT_S = max(0.0, args.heat)
     import herbert_hip as hb
     g = hb.Gpu(0)
