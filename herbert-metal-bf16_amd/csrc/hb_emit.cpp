@@ -60,6 +60,7 @@ hb_desc with_defaults(const hb_desc& in) {
         if (!d.rows) d.rows = 4;
         if (!d.unroll) d.unroll = 4;
         if (d.form == 1 || (d.form == 3 && d.rows != 32)) d.rows = 16;
+        if (d.form == 4 && d.rows != 8 && d.rows != 16) d.rows = 4;
         if (!d.mv_waves) d.mv_waves = 4;
     }
     return d;
@@ -209,9 +210,13 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
                           D("HB_BN", d.bn), D("HB_MFIRST", d.m_first ? 1 : 0)};
             return HB_OK;
         case HB_KIND_MATVEC: {
-            if (d.out > HB_OUT_SWIGLU || d.form > 3 || d.xsrc > HB_XSRC_NORM)
+            if (d.out > HB_OUT_SWIGLU || d.form > 4 || d.xsrc > HB_XSRC_NORM)
                 return fail(HB_ERR_INVALID, "matvec: out / form / xsrc out of range");
-            const bool mma = d.form == 1 || d.form == 3;
+            if (d.form == 4 && (d.mv_m > 8 || !d.split || d.k % (128 * d.split) || d.xsrc ||
+                                d.out == HB_OUT_SWIGLU || d.x_lds))
+                return fail(HB_ERR_UNSUPPORTED,
+                            "matvec (MFMA 4x4x4): m <= 8, K/split a multiple of 128, no fusions, no x_lds");
+            const bool mma = d.form == 1 || d.form == 3 || d.form == 4;
             if ((d.xsrc || d.out == HB_OUT_SWIGLU) && mma)
                 return fail(HB_ERR_UNSUPPORTED, "matvec: XSrc and Out::Swiglu fusions in the VALU forms");
             if (d.out == HB_OUT_SWIGLU && (d.rows % 2 || d.n % 2))
@@ -250,7 +255,9 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
                      d.out == HB_OUT_F32 ? "_f32" : d.out == HB_OUT_RESIDUAL ? "_res"
                                                   : d.out == HB_OUT_SWIGLU ? "_sw" : "",
                      d.rows, d.split, d.persist ? ("_p" + std::to_string(d.persist)).c_str() : "",
-                     d.mv_m, d.form == 1 ? "mfma" : d.form == 2 ? "dot2" : d.form == 3 ? "mfl" : "valu", d.unroll);
+                     d.mv_m,
+                     d.form == 1 ? "mfma" : d.form == 2 ? "dot2" : d.form == 3 ? "mfl" : d.form == 4 ? "mf4" : "valu",
+                     d.unroll);
             e->name = name;
             e->source = "matvec.hip";
             e->threads = 64 * d.mv_waves;

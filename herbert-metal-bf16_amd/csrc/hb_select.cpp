@@ -947,6 +947,34 @@ std::vector<std::pair<std::string, hb_desc>> mv_candidates(hb_engine* e, uint32_
             }
         }
     }
+    // The MFMA 4x4x4 form (W straight from memory as 4 rows x 256 bytes per
+    // load instruction, x in registers): waves sharing a row block's K so
+    // that each wave's x fits in at most 72 registers; 4, 8 or 16 W rows per
+    // wave and persistent workgroups (each wave's x serves more rows, which
+    // measured decisive at 4 and 8 rows: the lm_head at m=4 0.168 ms with
+    // one row block per wave, 0.126 with 1024 workgroups), within about 168
+    // registers (three waves a SIMD; 120 with 16-wave workgroups, whose
+    // limit is 128) (x, two row blocks of W in flight, the sums).
+    if (!fused && mv_m <= 8) {
+        const uint32_t mq = (mv_m + 3) / 4;
+        for (uint32_t waves : {4u, 8u, 16u})
+            for (uint32_t split : {1u, 2u, 4u, 8u}) {
+                if (waves == 16 && split < 8) continue;
+                if (split > waves || k % (128 * split)) continue;
+                const uint32_t li = k / split / 128;
+                if (li * mq > 18 || li < 2) continue;
+                for (uint32_t rows : {4u, 8u, 16u})
+                    for (uint32_t p : {0u, 256u, 1024u}) {
+                        const uint32_t tg = rows / 4, vg = li * mq * 4 + (p ? 2 : 1) * tg * li * 4 + tg * mq * 8;
+                        if (vg > (waves == 16 ? 120u : 168u) || (p == 0 && rows > 4) || (mv_m == 1 && p == 256)) continue;
+                        hb_desc d4 = desc(4, rows, split, p);
+                        d4.mv_waves = waves;
+                        v.emplace_back("mf4_r" + std::to_string(rows) + "k" + std::to_string(split) + "_w" +
+                                           std::to_string(waves) + (p ? "p" + std::to_string(p) : ""),
+                                       d4);
+                    }
+            }
+    }
     for (uint32_t split : splits)
         for (uint32_t p : pers) {
             if (fused) break;  // the fusions are VALU forms

@@ -32,6 +32,17 @@
 //    forms read it) and turned into the A operand through a wave-private
 //    LDS tile: the MFMA's arithmetic with the VALU forms' HBM access; its
 //    x (the B operand) from memory, or staged in LDS once per workgroup.
+//  4 (MFMA 4x4x4, 16 blocks): a wavefront computes ROWS (4, 8, 16) rows
+//    of W, in groups of 4, with
+//    v_mfma_f32_4x4x4_16b_bf16, its 16 blocks 16 slices of K: lane
+//    (b, j) = 4b + j loads W row j's elements 128c + 8b .. +7 (one load
+//    instruction reads 256 contiguous bytes of each of the 4 rows, whole
+//    128-byte lines) and holds x row j (and 4 + j) at the same elements, as
+//    the MFMA's B and A operands, the low and high 4 elements in two
+//    MFMAs: no LDS and no VALU arithmetic in the K loop.  The wave's x
+//    stays in registers for its K range; with PERSIST the next row block's
+//    W loads are issued before this one's MFMAs.  The 16 blocks' sums are
+//    added by DPP within each 16 lanes and two lane swaps across them.
 // Both: SPLIT wavefronts of a workgroup share a row block's K (contiguous
 // ranges); their partials are added in wave order through LDS.  PERSIST
 // > 0: that many workgroups loop over the row blocks.
@@ -62,10 +73,13 @@ constexpr u32 SPLIT = HB_SPLIT, U = HB_UNROLL;
 constexpr u32 WAVES = HB_WAVES, NT = 64 * WAVES;
 static_assert(WAVES == 4 || WAVES == 8 || WAVES == 16, "4, 8 or 16 waves");
 constexpr u32 GROUPS_PER_WG = WAVES / SPLIT;  // row blocks per workgroup
-#if !HB_MMA
+#if !HB_MMA && HB_FORM != 4
 constexpr u32 RB = HB_ROWS;                   // rows per row block
 #elif HB_FORM == 3
 constexpr u32 RB = HB_ROWS == 32 ? 32 : 16;   // one or two 16-row MFMA tiles
+#elif HB_FORM == 4
+constexpr u32 RB = HB_ROWS;                   // 4, 8 or 16: groups of the MFMA's 4 W rows
+static_assert(RB == 4 || RB == 8 || RB == 16, "MFMA 4x4x4 form: 4, 8 or 16 rows per wave");
 #else
 constexpr u32 RB = 16;
 #endif
@@ -106,6 +120,8 @@ constexpr u32 XST = HB_FORM == 3 ? K / 8 + 1 : K / 8;
 static_assert(WAVES % SPLIT == 0, "split divides the waves");
 static_assert(K % (8 * SPLIT) == 0 && KS % 8 == 0, "K split in whole chunks");
 static_assert(!HB_MMA || (MV <= 16 && KS % 32 == 0), "MFMA form: m <= 16, K steps of 32");
+static_assert(HB_FORM != 4 || (MV <= 8 && KS % 128 == 0 && HB_XSRC == 0 && !SWO && !HB_XLDS),
+              "MFMA 4x4x4 form: m <= 8, K/split a multiple of 128, no fusions, x in registers");
 
 // bf16(g * sigmoid(g) * u) as f32: swiglu's arithmetic (the SwiGLU kernels'
 // own expression, kernels.rs:256-261).
@@ -265,6 +281,122 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
     const u32 nwg = (NBLK + GROUPS_PER_WG - 1) / GROUPS_PER_WG;
     const u32 step = HB_PERSIST ? gridDim.x : nwg;
 
+#if HB_FORM == 4
+    constexpr u32 MQ = (MV + 3) / 4;  // quads of x rows
+    constexpr u32 TG = RB / 4;        // groups of 4 W rows per row block
+    constexpr u32 LI = KS / 128;      // load instructions per group
+    const u32 jr = lane & 3u, kb = (lane >> 2) * 8;
+    // x: lane (b, j) holds x row 4q + j, elements k0 + 128c + 8b .. +7: the
+    // A operand of quad q (A row i = lane % 4).  Rows past m read row m-1:
+    // they only reach D's rows past m, which are never stored.
+    u32x4 xr[MQ][LI];
+#pragma unroll
+    for (u32 q = 0; q < MQ; q++) {
+        const u32 row = 4 * q + jr < m ? 4 * q + jr : m - 1;
+        const u16* xp = x + (u64)row * K + k0 + kb;
+#pragma unroll
+        for (u32 c = 0; c < LI; c++) xr[q][c] = *(const u32x4*)(xp + 128 * c);
+    }
+    // W rows n0 + 4t + j (rows past N read row N-1; their sums are never
+    // stored).
+    auto wload = [&](u32x4 (&v)[TG][LI], u32 wg) HB_INLINE2 {
+#pragma unroll
+        for (u32 t = 0; t < TG; t++) {
+            const u32 n = (wg * GROUPS_PER_WG + gi) * RB + 4 * t + jr;
+            const u16* wr = W + (u64)(n < N ? n : N - 1) * K + k0 + kb;
+#pragma unroll
+            for (u32 c = 0; c < LI; c++) v[t][c] = __builtin_nontemporal_load((const u32x4*)(wr + 128 * c));
+        }
+    };
+    typedef __attribute__((ext_vector_type(4))) short s16x4;
+    auto lo4 = [](u32x4 v) HB_INLINE2 { return __builtin_bit_cast(s16x4, u32x2{v.x, v.y}); };
+    auto hi4 = [](u32x4 v) HB_INLINE2 { return __builtin_bit_cast(s16x4, u32x2{v.z, v.w}); };
+    auto block4 = [&](const u32x4 (&v)[TG][LI], u32 wg) HB_INLINE2 {
+        const u32 n0 = (wg * GROUPS_PER_WG + gi) * RB;
+        // D of block b: lane 4b + j, register i = the sum of x row 4q + i and
+        // W row n0 + 4t + j over block b's elements.
+        f32x4 acc[TG][MQ][2];
+#pragma unroll
+        for (u32 t = 0; t < TG; t++)
+#pragma unroll
+            for (u32 q = 0; q < MQ; q++) acc[t][q][0] = acc[t][q][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (u32 c = 0; c < LI; c++)
+#pragma unroll
+            for (u32 t = 0; t < TG; t++)
+#pragma unroll
+                for (u32 q = 0; q < MQ; q++) {
+                    acc[t][q][0] =
+                        __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(lo4(xr[q][c]), lo4(v[t][c]), acc[t][q][0], 0, 0, 0);
+                    acc[t][q][1] =
+                        __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(hi4(xr[q][c]), hi4(v[t][c]), acc[t][q][1], 0, 0, 0);
+                }
+        // The 16 blocks' sum: the 4 of each 16 lanes by DPP (row rotations
+        // by 4 and 8), then lane (r, i, j) keeps register i and the 4 rows of
+        // 16 lanes are added (xor 16, xor 32).  Lane l < 16 * MQ ends with
+        // x row 4 * (l / 16) + (l / 4) % 4, W row n0 + 4t + l % 4.
+        const u32 qd = (lane >> 2) & 3u;
+        float mine[TG];
+#pragma unroll
+        for (u32 t = 0; t < TG; t++) {
+            mine[t] = 0.0f;
+#pragma unroll
+            for (u32 q = 0; q < MQ; q++) {
+                const f32x4 a = acc[t][q][0] + acc[t][q][1];
+                float r = 0.0f;
+#pragma unroll
+                for (u32 i = 0; i < 4; i++) {
+                    float v1 = dpp_add<0x124>(a[i]);  // row_ror:4
+                    v1 = dpp_add<0x128>(v1);          // row_ror:8
+                    r = qd == i ? v1 : r;
+                }
+                r += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, r), 0x401F));
+                r += __shfl_xor(r, 32, 64);
+                if (lane >> 4 == q) mine[t] = r;
+            }
+        }
+        const bool owner = lane < 16 * MQ;
+        if constexpr (SPLIT > 1) {
+            if (owner)
+#pragma unroll
+                for (u32 t = 0; t < TG; t++) part[(wave * TG + t) * 32 + lane] = mine[t];
+            __syncthreads();
+            if (sp == 0 && owner) {
+#pragma unroll
+                for (u32 t = 0; t < TG; t++) {
+                    float s = 0.0f;
+#pragma unroll
+                    for (u32 q = 0; q < SPLIT; q++) s += part[((gi * SPLIT + q) * TG + t) * 32 + lane];
+                    mine[t] = s;
+                }
+            }
+        }
+        const u32 mr = 4 * (lane >> 4) + qd;
+        if (sp == 0 && owner && mr < m)
+#pragma unroll
+            for (u32 t = 0; t < TG; t++) {
+                const u32 nn = n0 + 4 * t + jr;
+                if (nn < N) store_out(y, (u64)mr * N + nn, mine[t]);
+            }
+        if constexpr (SPLIT > 1) __syncthreads();  // part[] reused by the next block
+    };
+    u32x4 va[TG][LI];
+    u32 wg = blockIdx.x;
+    if (wg < nwg) wload(va, wg);
+    if constexpr (HB_PERSIST == 0) {
+        if (wg < nwg) block4(va, wg);
+    } else while (wg < nwg) {
+        u32x4 vb[TG][LI];
+        const u32 w2 = wg + step;
+        if (w2 < nwg) wload(vb, w2);
+        block4(va, wg);
+        if (w2 >= nwg) break;
+        const u32 w3 = w2 + step;
+        if (w3 < nwg) wload(va, w3);
+        block4(vb, w2);
+        wg = w3;
+    }
+#else
     for (u32 wg = blockIdx.x; wg < nwg; wg += step) {
         const u32 blk = wg * GROUPS_PER_WG + gi;
         const u32 n0 = blk * RO;  // first output row
@@ -579,4 +711,5 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(const u16* __restrict__
 #endif
         if constexpr (SPLIT > 1) __syncthreads();  // part[] reused by the next block
     }
+#endif
 }

@@ -286,7 +286,8 @@ def matvec(kdim, n, out, mv_m=1, rows=4, split=1, persist=0, form=0, unroll=4, x
            plus_one=False, x_lds=False, waves=0):
     """matvec / matvec_split (kernels.rs:146, 502, 640): y[m][n] = x[m][k].W^T for m <= mv_m;
     form 0 the VALU layout (rows per wave), 1 the MFMA layout (16 rows per wave), 2 the VALU
-    layout with v_dot2, 3 the MFMA form with W read in row order through LDS; xsrc / out Swiglu the decode fusions (VALU forms); x_lds the x rows
+    layout with v_dot2, 3 the MFMA form with W read in row order through LDS, 4 the 4x4x4 MFMA
+    form (4 rows per wave, W loaded straight into the operand, x in registers); xsrc / out Swiglu the decode fusions (VALU forms); x_lds the x rows
     staged in LDS once per workgroup (VALU forms); waves: wavefronts per workgroup (0 = 4, 8, 16;
     with x_lds up to 144 KiB of x)."""
     import struct

@@ -131,7 +131,9 @@ typedef struct hb_desc {
      * v_dot2_f32_bf16 (two products added per instruction, no conversion),
      * 3 MFMA with W loaded in row order and turned into the A operand
      * through a per-wave LDS tile (unroll 4, 8 or 16; rows 32: two 16-row
-     * MFMA tiles sharing each x fragment). */
+     * MFMA tiles sharing each x fragment), 4 v_mfma_f32_4x4x4_16b_bf16 with
+     * 4 W rows per wave, its 16 blocks slices of K, W loaded straight into
+     * the operand (m <= 8, K/split a multiple of 128, no fusions). */
     uint32_t mv_m, split, persist, rows, form;
     /* MoE: slots per row (top_k), experts, the tile table's capacity
      * (moe_tiles, prefill.rs:832-835), rows of the largest block. */

@@ -330,3 +330,64 @@ def test_matvec_x_in_lds_fusions(gpu, m):
     got = run_mv_fused(gpu, x, w2, hb.Out.Swiglu, None, 2, x_lds=True, **f)
     ref = run_mv_fused(gpu, x, w2, hb.Out.Swiglu, None, 2, **f)
     assert np.array_equal(got, ref), "Out::Swiglu: x in LDS differs from x from memory"
+
+
+# ---- form 4: v_mfma_f32_4x4x4_16b_bf16, W loaded straight into the B
+# operand (4 rows x 256 bytes per load instruction), x in registers; the 16
+# blocks' sums added by DPP and lane swaps, the split waves' partials in wave
+# order through LDS.
+
+MF4_FORMS = {"mf4_k1": dict(form=4, split=1), "mf4_k2": dict(form=4, split=2),
+             "mf4_k4_w8_p": dict(form=4, split=4, waves=8, persist=1024),
+             "mf4_k8_w16": dict(form=4, split=8, waves=16),
+             "mf4_k2_p3": dict(form=4, split=2, persist=3),
+             "mf4_r8_k4_p256": dict(form=4, rows=8, split=4, persist=256),
+             "mf4_r8_k8_w8_p7": dict(form=4, rows=8, split=8, waves=8, persist=7),
+             "mf4_r16_k4_w8_p256": dict(form=4, rows=16, split=4, waves=8, persist=256)}
+
+
+def mf4_ok(k, split, mv_m):
+    """The form's own limits and the candidate list's: K/split a multiple of
+    128, x of a wave in at most 72 registers."""
+    if k % (128 * split):
+        return False
+    return (k // split // 128) * ((mv_m + 3) // 4) <= 18
+
+
+@pytest.mark.parametrize("mv_m,m", [(8, 8), (8, 5), (4, 4), (4, 3), (1, 1)])
+@pytest.mark.parametrize("form", sorted(MF4_FORMS))
+@pytest.mark.parametrize("name,k,n,out", SHAPES)
+def test_matvec_mf4_config3_layer(gpu, name, k, n, out, form, mv_m, m):
+    f = MF4_FORMS[form]
+    if not mf4_ok(k, f["split"], mv_m):
+        pytest.skip("K/split not a whole number of 128-element loads, or x over 64 registers")
+    x = hb.normal_bf16(0x5EED0013, 1.0, (m, k))
+    w = hb.normal_bf16(0x5EED0014, 0.02, (n, k))
+    y0 = hb.normal_bf16(19, 1.0, (m, n)) if out == 2 else None
+    got = run_mv(gpu, x, w, out, y0, mv_m=mv_m, **f)
+    want = orc.gemm(x, w, out, y0)
+    acc = orc.gemm(x, w, orc.OUT_F32) if out == 2 else None
+    check_close(got, want, k, abs_products(x, w), "%s %s m=%d/%d" % (name, form, m, mv_m), acc=acc)
+
+
+@pytest.mark.parametrize("rows", [4, 16])
+@pytest.mark.parametrize("persist", [0, 5])
+@pytest.mark.parametrize("k,n,split", [(1024, 100, 1), (512, 33, 2), (2048, 6, 4), (256, 4097, 1)])
+def test_matvec_mf4_ragged(gpu, k, n, split, persist, rows):
+    """N not a multiple of the 4-row block (rows past N clamped, never
+    stored), fewer row blocks than waves, f32 out; x rows 0..m-1 of 8."""
+    for m in (1, 2, 7):
+        x = hb.normal_bf16(0x5EED0015 + m, 1.0, (m, k))
+        w = hb.normal_bf16(0x5EED0016, 0.02, (n, k))
+        got = run_mv(gpu, x, w, 1, form=4, rows=rows, split=split, persist=persist, waves=8 if split > 4 else 4)
+        check_close(got, orc.gemm(x, w, orc.OUT_F32), k, abs_products(x, w),
+                    "mf4 %dx%d r%d k%d p%d m=%d" % (k, n, rows, split, persist, m))
+
+
+@pytest.mark.parametrize("m", [1, 4, 8])
+def test_matvec_mf4_lm_head(gpu, m):
+    k, n = 2560, 151936
+    x = hb.normal_bf16(0x5EED0005, 1.0, (m, k))
+    w = hb.normal_bf16(0x5EED0006, 0.02, (n, k))
+    got = run_mv(gpu, x, w, 0, mv_m=m, form=4, split=4, waves=8, persist=1024)
+    check_close(got, orc.gemm(x, w), k, abs_products(x, w), "lm_head mf4 m=%d" % m)
