@@ -157,6 +157,7 @@ HB_DEV void store4(void* Yv, u64 at, float v0, float v1, float v2, float v3) {
     }
 }
 
+#define HB_EPI_NT 1  // non-temporal output stores
 #include "gemm_epi.h"
 
 #define HB_INLINE __attribute__((always_inline))
