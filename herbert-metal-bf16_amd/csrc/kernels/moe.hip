@@ -37,6 +37,57 @@ constexpr u32 E = HB_E, TOPK = HB_TOPK, D = HB_D;
 static_assert(E % 64 == 0 && E <= 1024 && TOPK <= 64, "route: experts a multiple of 64");
 constexpr u32 P = E / 64;
 
+// The wave's maximum, and its argmax (the largest value, the lowest index on
+// a tie): within each 16 lanes by DPP (quad swaps, then row rotations by 4
+// and 8), then the four rows' results read as scalars.  Both are the same for
+// any order of combination (a max; a total order on (value, -index)), so
+// they equal the xor-butterfly's results without its LDS-crossbar round
+// trips, which made the top-k loop a chain of 96 shuffles.
+template <int CTRL>
+HB_DEV u32 dpp_u32(u32 v) {
+    return (u32)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, true);
+}
+template <int CTRL>
+HB_DEV float dpp_f32(float v) {
+    return __builtin_bit_cast(float, dpp_u32<CTRL>(__builtin_bit_cast(u32, v)));
+}
+HB_DEV float lane_f32(float v, u32 l) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+HB_DEV float wave_max(float v) {
+    float o;
+    o = dpp_f32<0xB1>(v);  v = o > v ? o : v;   // quad_perm [1,0,3,2]
+    o = dpp_f32<0x4E>(v);  v = o > v ? o : v;   // quad_perm [2,3,0,1]
+    o = dpp_f32<0x124>(v); v = o > v ? o : v;   // row_ror:4
+    o = dpp_f32<0x128>(v); v = o > v ? o : v;   // row_ror:8
+    float m = lane_f32(v, 0);
+#pragma unroll
+    for (u32 r = 1; r < 4; r++) {
+        o = lane_f32(v, 16 * r);
+        m = o > m ? o : m;
+    }
+    return m;
+}
+HB_DEV void wave_argmax(float& best, u32& idx) {
+    auto take = [&](float ob, u32 oi) {
+        if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
+    };
+    take(dpp_f32<0xB1>(best), dpp_u32<0xB1>(idx));
+    take(dpp_f32<0x4E>(best), dpp_u32<0x4E>(idx));
+    take(dpp_f32<0x124>(best), dpp_u32<0x124>(idx));
+    take(dpp_f32<0x128>(best), dpp_u32<0x128>(idx));
+    float b = lane_f32(best, 0);
+    u32 i = __builtin_amdgcn_readlane(idx, 0);
+#pragma unroll
+    for (u32 r = 1; r < 4; r++) {
+        const float ob = lane_f32(best, 16 * r);
+        const u32 oi = __builtin_amdgcn_readlane(idx, 16 * r);
+        if (ob > b || (ob == b && oi < i)) { b = ob; i = oi; }
+    }
+    best = b;
+    idx = i;
+}
+
 extern "C" __global__ __launch_bounds__(256) void HB_NAME(const u16* __restrict__ scores,
                                                             u32* __restrict__ route, u32 rows) {
     const u32 lane = threadIdx.x & 63u;
@@ -49,11 +100,7 @@ extern "C" __global__ __launch_bounds__(256) void HB_NAME(const u16* __restrict_
     float mx = v[0];
 #pragma unroll
     for (u32 p = 1; p < P; p++) mx = v[p] > mx ? v[p] : mx;
-#pragma unroll
-    for (int sh = 32; sh >= 1; sh >>= 1) {
-        float o = __shfl_xor(mx, sh, 64);
-        mx = o > mx ? o : mx;
-    }
+    mx = wave_max(mx);
     float e[P], t[P];
 #pragma unroll
     for (u32 p = 0; p < P; p++) e[p] = t[p] = hb_expf(v[p] - mx);
@@ -78,12 +125,7 @@ extern "C" __global__ __launch_bounds__(256) void HB_NAME(const u16* __restrict_
 #pragma unroll
         for (u32 p = 0; p < P; p++)
             if (pr[p] > best) { best = pr[p]; idx = lane + 64 * p; }
-#pragma unroll
-        for (int sh = 32; sh >= 1; sh >>= 1) {
-            float ob = __shfl_xor(best, sh, 64);
-            u32 oi = __shfl_xor(idx, sh, 64);
-            if (ob > best || (ob == best && oi < idx)) { best = ob; idx = oi; }
-        }
+        wave_argmax(best, idx);
         chosen[i] = idx;
         vals[i] = best;
 #pragma unroll
