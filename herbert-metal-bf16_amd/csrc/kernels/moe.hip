@@ -163,6 +163,8 @@ extern "C" __global__ __launch_bounds__(256) void HB_NAME(const u16* __restrict_
 // in registers for both passes; beyond that they are read in each pass.
 static_assert(E <= 1024, "sort: at most 1024 experts");
 constexpr u32 BM = HB_BM, NW = 16;
+// Histograms in use: one per wave (scan form), one shared (atomic form).
+constexpr u32 NH = HB_OP == 2 ? NW : 1;
 constexpr u32 PMAX = HB_RMAX * TOPK, PER = (PMAX + 1023) / 1024;
 constexpr bool HOLD = PER <= 32;
 constexpr u32 EPL = (E + 63) / 64;  // experts per lane of the scans
@@ -171,7 +173,7 @@ extern "C" __global__ __launch_bounds__(1024) void HB_NAME(const u32* __restrict
                                                              const u32* __restrict__ route,
                                                              u32* __restrict__ list,
                                                              u32* __restrict__ tiles, u32 m_launch) {
-    __shared__ u32 hist[NW][E];  // per wave per expert: count, then the wave's cursor
+    __shared__ u32 hist[NH][E];  // per wave (or shared) per expert: count, then the cursor
     __shared__ u32 start[E], tstart[E + 1], cnt[E];
     const u32 tid = threadIdx.x, lane = tid & 63u, w = tid >> 6;
     const u32 m = rows_of_state(state, m_launch);
@@ -196,7 +198,7 @@ extern "C" __global__ __launch_bounds__(1024) void HB_NAME(const u32* __restrict
 #pragma unroll
         for (u32 k = 0; k < PER; k++) ex[k] = in_k(k) ? expert_of(pair_k(k)) : E;
     }
-    for (u32 i = tid; i < NW * E; i += 1024) (&hist[0][0])[i] = 0;
+    for (u32 i = tid; i < NH * E; i += 1024) (&hist[0][0])[i] = 0;
     __syncthreads();
     if constexpr (HOLD) {
 #pragma unroll
@@ -209,7 +211,7 @@ extern "C" __global__ __launch_bounds__(1024) void HB_NAME(const u32* __restrict
     // Per expert: its count, and each wave's offset inside the expert.
     for (u32 x = tid; x < E; x += 1024) {
         u32 s = 0;
-        for (u32 q = 0; q < NW; q++) {
+        for (u32 q = 0; q < NH; q++) {
             u32 c = hist[q][x];
             hist[q][x] = s;
             s += c;
@@ -264,7 +266,7 @@ extern "C" __global__ __launch_bounds__(1024) void HB_NAME(const u32* __restrict
             t[2] = c - j * BM < BM ? c - j * BM : BM;
         }
 #pragma unroll 1
-        for (u32 q = 0; q < NW; q++) hist[q][x] += start[x];
+        for (u32 q = 0; q < NH; q++) hist[q][x] += start[x];
     }
     __syncthreads();
 #if HB_OP == 2
