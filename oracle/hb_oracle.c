@@ -28,7 +28,10 @@
  *   - hbo_combine: exact-term sums (f64), top_k 1 with weight 1 (identity),
  *     and two hand-worked cases that fix the slot order, the rounding of
  *     each partial sum and the rounding of each product;
- *   and the swiglu / combine checks are shown to fail on builds of this
+ *   - hbo_gather_rows: X rows that carry their own index; the identity list
+ *     repeats each row top_k times (np.repeat), top_k = 1 is a row
+ *     permutation (np.take), and each token's top_k pairs read its row;
+ *   and the swiglu / combine / gather checks are shown to fail on builds of this
  *   file with one deliberate error each (tests/test_oracle_mutants.py).
  *
  * Numerical contract: bf16 operands widened

@@ -373,6 +373,44 @@ def combine_pins(combine):
     assert bf16_to_f32(out)[0, 0] == 1.015625, "combine product rounding"
 
 
+def gather_pins(gather):
+    """Pins moe_gather (prefill.rs:579-610): XS[p] = X[list[p] / top_k],
+    with every X row carrying its own index so a misread row shows.
+    Checked against what the mapping fixes without restating it: the
+    identity list repeats each X row top_k times (np.repeat); top_k = 1 is a
+    plain row permutation (np.take); for any permutation of the pairs, each
+    token's row appears exactly top_k times and the pairs of one token
+    (consecutive pair ids, row*top_k + slot) all read that token's row."""
+    rng = np.random.default_rng(21)
+    rows, hidden = 37, 24
+    x = np.empty((rows, hidden), np.uint16)
+    x[:, 0::2] = np.arange(rows, dtype=np.uint16)[:, None]          # the row's id
+    x[:, 1::2] = (0x4000 + np.arange(hidden // 2, dtype=np.uint16))[None, :]  # the column's id
+    for top_k in (1, 2, 8):
+        pairs = rows * top_k
+        ident = np.arange(pairs, dtype=np.uint32)
+        assert np.array_equal(gather(x, ident, top_k), np.repeat(x, top_k, axis=0)), \
+            "identity list: each row top_k times (top_k=%d)" % top_k
+        perm = rng.permutation(pairs).astype(np.uint32)
+        xs = gather(x, perm, top_k)
+        assert xs.shape == (pairs, hidden)
+        assert np.all(xs[:, 1::2] == x[0, 1::2]), "columns kept in place"
+        ids = xs[:, 0].astype(np.int64)
+        assert np.array_equal(np.bincount(ids, minlength=rows), np.full(rows, top_k)), \
+            "each token's row exactly top_k times (top_k=%d)" % top_k
+        inv = np.argsort(perm)   # where pair q landed
+        for r in range(rows):
+            got = ids[inv[r * top_k:(r + 1) * top_k]]
+            assert np.all(got == r), "pairs of token %d read rows %s" % (r, got)
+        if top_k == 1:
+            assert np.array_equal(xs, np.take(x, perm, axis=0)), "top_k=1 is a row permutation"
+        assert np.array_equal(xs[:, 0::2], np.repeat(ids[:, None], hidden // 2, axis=1).astype(np.uint16))
+
+
+def test_gather_rows_pinned():
+    gather_pins(lambda x, list_, k: orc.gather_rows(x, list_, k))
+
+
 def test_swiglu_pinned():
     swiglu_pins(lambda gu, n: orc.swiglu(gu, n))
 
