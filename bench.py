@@ -56,6 +56,7 @@ M = 2048
 LAYER = [("qkv", 2560, 4608, 0), ("o", 4096, 2560, 2), ("gate_up", 2560, 18432, 0),
          ("down", 9216, 2560, 2)]
 LM_HEAD = ("lm_head", 2560, 151936, 0)
+QKV_REAL = [("qkv10240", 2560, 10240, 0)]
 CONFIG1 = [("gemm", 1024, 3584, 0)]
 CONFIG4 = [("qkv", 5120, 7168, 0), ("gate_up", 5120, 34816, 0), ("down", 17408, 5120, 2),
            ("lm_head", 5120, 151936, 0)]
@@ -377,7 +378,8 @@ def gemm_set(g, e, hb, shapes, m, steps, seed):
 def bench_prefill_more(g, e, hb, steps):
     """The other prefill cases of BASELINE.json: config 1 (one GEMM, M=512,
     K=1024, N=3584), config 2 at M=512 and 1024 (the step above is M=2048),
-    config 4 (27B-class shapes at M=2048, lm_head included)."""
+    config 4 (27B-class shapes at M=2048, lm_head included), and the
+    reference's real 4B fused QKV (2560 -> 10240) at M=512, 1024, 2048."""
     steps = max(3, min(steps, 10))
     res = {"config1": gemm_set(g, e, hb, CONFIG1, 512, steps, 0x5EED0001)}
     # config 1's kernel name is its own (no other case has 1024 x 3584), so
@@ -390,6 +392,12 @@ def bench_prefill_more(g, e, hb, steps):
     c1["traffic"] = tr["bytes"] if tr else None
     for m in (512, 1024):
         res["config2_m%d" % m] = gemm_set(g, e, hb, LAYER, m, steps, SEED)
+    # The reference's real Qwen3.5-4B fused QKV width: q_width = 2 * heads *
+    # head_dim carries the output gate, 8192 + 2 * 1024 = 10240 columns
+    # (qwen_kernels.rs:41-51, probe.rs:738-741), where BASELINE's config 2
+    # names 2560 + 2 * 1024: reported beside it, at each block size.
+    for m in (512, 1024, 2048):
+        res["qkv10240_m%d" % m] = gemm_set(g, e, hb, QKV_REAL, m, steps, SEED + 40)
     res["config4_m2048"] = gemm_set(g, e, hb, CONFIG4, M, steps, 0x5EED0004)
     return res
 

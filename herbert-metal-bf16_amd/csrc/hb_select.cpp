@@ -611,7 +611,8 @@ extern "C" {
 
 int hb_engine_open(hb_gpu* g, const char* tune, hb_engine** out) {
     *out = nullptr;
-    if (!g) return fail(HB_ERR_INVALID, "hb_engine_open: no context");
+    // No context: a host-only engine (the --tune table, the log and the
+    // host-driven autotune_chunk); the kernel selections refuse.
     hb_engine* e = new hb_engine();
     e->g = g;
     std::string err;
@@ -675,6 +676,7 @@ int hb_engine_add_gemm_candidate(hb_engine* e, const char* name, const hb_desc* 
 }
 
 int hb_engine_log_summary(hb_engine* e) {
+    if (!e->g) return fail(HB_ERR_INVALID, "log_summary: an engine without a context");
     e->logf("[hip] %zu kernels compiled in %.1f s, GEMMs and blocks timed in %.1f s",
             e->g->kernels.size(), e->g->compile_seconds, e->autotune_seconds);
     return HB_OK;
@@ -711,6 +713,7 @@ int hb_engine_gemm_candidates(hb_engine* e, uint32_t k, uint32_t n, uint32_t out
 
 int hb_engine_gemm(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, hb_range state,
                    hb_range w, hb_range x, hb_range y, uint32_t m, int32_t* kernel) {
+    if (!e->g) return fail(HB_ERR_INVALID, "gemm: an engine without a context");
     const Tune& t = e->t;
     bool mf = t["gemm.mfirst"] != 0;
     int rc;
@@ -777,6 +780,7 @@ int hb_engine_gemm(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, hb_range 
 int hb_engine_gate_up(hb_engine* e, uint32_t h, uint32_t inter, hb_range state, hb_range w,
                       hb_range x, hb_range gu, hb_range hout, uint32_t m, int32_t* gemm_kernel,
                       int32_t* swiglu_kernel) {
+    if (!e->g) return fail(HB_ERR_INVALID, "gate_up: an engine without a context");
     const Tune& t = e->t;
     int rc;
     *gemm_kernel = *swiglu_kernel = -1;
@@ -835,6 +839,7 @@ int hb_engine_gate_up(hb_engine* e, uint32_t h, uint32_t inter, hb_range state, 
 
 int hb_engine_matvec(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, uint32_t mv_m,
                      const hb_range* ws, uint32_t nws, hb_range x, hb_range y, int32_t* kernel) {
+    if (!e->g) return fail(HB_ERR_INVALID, "matvec: an engine without a context");
     return hb_engine_matvec_fused(e, k, n, out, HB_XSRC_PLAIN, 0, 0, mv_m, ws, nws, x, y,
                                   hb_range{}, kernel);
 }
@@ -1001,6 +1006,7 @@ int hb_engine_matvec_candidates(hb_engine* e, uint32_t k, uint32_t n, uint32_t o
 int hb_engine_matvec_fused(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, uint32_t xsrc,
                            uint32_t eps_bits, uint32_t plus_one, uint32_t mv_m, const hb_range* ws,
                            uint32_t nws, hb_range x, hb_range y, hb_range norm_w, int32_t* kernel) {
+    if (!e->g) return fail(HB_ERR_INVALID, "matvec_fused: an engine without a context");
     const Tune& t = e->t;
     if (!nws) return fail(HB_ERR_INVALID, "matvec: no weights");
     // A fusion (kernels.rs:236-290): the VALU forms, rows in gate/up pairs
@@ -1081,6 +1087,7 @@ int hb_engine_matvec_fused(hb_engine* e, uint32_t k, uint32_t n, uint32_t out, u
 int hb_engine_experts(hb_engine* e, uint32_t experts, uint32_t top_k, uint32_t hidden,
                       uint32_t inter, uint32_t m, const hb_moe_io* io, int32_t kernels[4],
                       uint32_t* bm_out) {
+    if (!e->g) return fail(HB_ERR_INVALID, "experts: an engine without a context");
     const Tune& t = e->t;
     bool mf = t["gemm.mfirst"] != 0;
     int rc;
@@ -1269,6 +1276,79 @@ int hb_engine_experts(hb_engine* e, uint32_t experts, uint32_t top_k, uint32_t h
         }
     }
     e->logf("[autotune] experts, %u rows -> tiles of %u rows", m, *bm_out);
+    return HB_OK;
+}
+
+// autotune_chunk (qwen.rs:2962-3010): the candidates 1024, 2048, 4096, 8192
+// below prefill.block and prefill.block itself; the host's first block of
+// cands[0] rows run until auto.heat ms of GPU time have passed; then three
+// rounds, the order reversed every other one, each candidate's prompt of
+// prefill.block rows cut by blocks_of and its blocks' GPU times summed; the
+// median of each; the fastest kept (the first on a tie, as min_by does).
+int hb_engine_autotune_chunk(hb_engine* e, const hb_prefill_host* host, uint32_t* chunk) {
+    if (!host || !host->block_in || !chunk) return fail(HB_ERR_INVALID, "autotune_chunk: host and chunk");
+    const auto started = std::chrono::steady_clock::now();
+    const uint32_t block = e->t["prefill.block"];
+    std::vector<uint32_t> cands;
+    for (uint32_t c : {1024u, 2048u, 4096u, 8192u})
+        if (c < block) cands.push_back(c);
+    cands.push_back(block);
+    *chunk = block;
+    if (cands.size() < 2) return HB_OK;
+    auto reset = [&]() -> int {
+        if (host->reset && host->reset(host->ctx))
+            return fail(HB_ERR_INVALID, "autotune_chunk: the host's reset failed");
+        return HB_OK;
+    };
+    auto run = [&](uint32_t start, uint32_t rows, double* s) -> int {
+        *s = 0.0;
+        if (host->block_in(host->ctx, start, rows, s))
+            return fail(HB_ERR_INVALID, "autotune_chunk: the host's block_in failed over " +
+                                            std::to_string(rows) + " rows at " + std::to_string(start));
+        return HB_OK;
+    };
+    int rc;
+    const double heat = e->t["auto.heat"] * 1e-3;
+    double warmed = 0.0, s;
+    do {
+        if ((rc = reset()) || (rc = run(0, cands[0], &s))) return rc;
+        warmed += s;
+    } while (warmed < heat);
+    std::vector<std::vector<double>> times(cands.size());
+    std::vector<uint32_t> starts, rows;
+    for (int round = 0; round < 3; round++)
+        for (size_t j = 0; j < cands.size(); j++) {
+            const size_t i = round % 2 == 0 ? j : cands.size() - 1 - j;
+            if ((rc = reset())) return rc;
+            const uint32_t nb = hb_blocks_of(block, cands[i], nullptr, nullptr, 0);
+            starts.resize(nb);
+            rows.resize(nb);
+            hb_blocks_of(block, cands[i], starts.data(), rows.data(), nb);
+            double t = 0.0;
+            for (uint32_t b = 0; b < nb; b++) {
+                if ((rc = run(starts[b], rows[b], &s))) return rc;
+                t += s;
+            }
+            times[i].push_back(t);
+        }
+    std::vector<double> med(cands.size());
+    size_t best = 0;
+    std::string line;
+    for (size_t i = 0; i < cands.size(); i++) {
+        std::sort(times[i].begin(), times[i].end());
+        med[i] = times[i][times[i].size() / 2];
+        if (med[i] < med[best]) best = i;
+        char one[64];
+        snprintf(one, sizeof one, "%s%u %.3f ms", i ? ", " : "", cands[i], med[i] * 1e3);
+        line += one;
+    }
+    if ((rc = reset())) return rc;
+    *chunk = cands[best];
+    e->logf("[autotune] blocks over %u rows, every layer, heated %.1f s, median of 3 rounds: %s -> %u", block,
+            warmed, line.c_str(), cands[best]);
+    e->autotune_seconds += std::chrono::duration<double>(std::chrono::steady_clock::now() - started).count();
+    e->timed = true;
+    e->last_timed = std::chrono::steady_clock::now();
     return HB_OK;
 }
 

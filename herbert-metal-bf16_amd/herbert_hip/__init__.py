@@ -33,6 +33,10 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(os.path.dirname(_HERE), "libherbert_hip.so")
 
 
+# Status codes (include/herbert_hip.h).
+HB_ERR_INVALID, HB_ERR_HIP, HB_ERR_COMPILE, HB_ERR_UNSUPPORTED, HB_ERR_NO_DEVICE = -1, -2, -3, -4, -5
+
+
 class HerbertError(RuntimeError):
     """A failing library call: the status code and the library's message."""
 
@@ -432,8 +436,9 @@ class Engine:
     [autotune] log."""
 
     def __init__(self, gpu, tune=""):
+        """gpu None: a host-only engine (tune, log, autotune_chunk)."""
         h = _P()
-        check(lib.hb_engine_open(gpu.h, tune.encode(), ctypes.byref(h)))
+        check(lib.hb_engine_open(gpu.h if gpu is not None else None, tune.encode(), ctypes.byref(h)))
         self.h = h
         self.gpu = gpu
 
@@ -769,6 +774,52 @@ class Checkpoint:
         return b.value
 
 
+_BLOCK_IN = ctypes.CFUNCTYPE(ctypes.c_int, _P, _u32, _u32, ctypes.POINTER(ctypes.c_double))
+_RESET = ctypes.CFUNCTYPE(ctypes.c_int, _P)
+
+
+class PrefillHost(ctypes.Structure):
+    """hb_prefill_host: the host's block_in and reset, for autotune_chunk."""
+    _fields_ = [("ctx", _P), ("block_in", _BLOCK_IN), ("reset", _RESET)]
+
+
+lib.hb_engine_autotune_chunk.argtypes = [_P, ctypes.POINTER(PrefillHost), ctypes.POINTER(_u32)]
+
+
+def autotune_chunk(engine, block_in, reset=None):
+    """autotune_chunk (qwen.rs:2962-3010) through the library's
+    hb_engine_autotune_chunk: `block_in(start, rows)` runs one block of the
+    prompt and returns its GPU seconds, `reset()` restores what a block
+    updates in place.  Returns the chosen rows per block (the library logs
+    the reference's "[autotune] blocks over ..." line)."""
+    err = []
+
+    def _blk(_ctx, start, rows, out):
+        try:
+            out[0] = float(block_in(int(start), int(rows)))
+            return 0
+        except Exception as ex:  # reported after the call: ctypes cannot raise through C
+            err.append(ex)
+            return 1
+
+    def _rst(_ctx):
+        try:
+            if reset is not None:
+                reset()
+            return 0
+        except Exception as ex:
+            err.append(ex)
+            return 1
+
+    host = PrefillHost(None, _BLOCK_IN(_blk), _RESET(_rst))
+    chunk = _u32()
+    rc = lib.hb_engine_autotune_chunk(engine.h, ctypes.byref(host), ctypes.byref(chunk))
+    if err:
+        raise err[0]
+    check(rc)
+    return chunk.value
+
+
 def blocks_of(n, chunk):
     """blocks_of (qwen.rs:3017-3027): [(start, rows)] of a prompt of n rows."""
     cap = n // 64 + 2
@@ -815,20 +866,25 @@ class PrefillMlp:
         """The ops of a prompt of n rows of the residual stream `x` (a buffer
         of [n][hidden] bf16, updated in place); `states`: one state buffer per
         block (blocks_of(n, chunk)), state[3] its rows."""
-        h, b, w = self.h, self.buf, self.w
         ops = []
         for (start, rows), st in zip(blocks_of(n, chunk or self.chunk), states):
-            m = min(bk for bk in self.buckets if bk >= rows)
-            gu_k, sw_k, dn_k = self.kern[m]
-            xr = r(x, start * h * 2, rows * h * 2)
-            s = r(st)
-            ops.append(Op(self.norm_k, [xr, r(w["post_norm"]), r(b["xn"])], rows))
-            if sw_k >= 0:
-                ops.append(Op(gu_k, [s, r(w["gate_up"]), r(b["xn"]), r(b["gu"]), s, s], rows))
-                ops.append(Op(sw_k, [r(b["gu"]), r(b["hh"])], rows))
-            else:
-                ops.append(Op(gu_k, [s, r(w["gate_up"]), r(b["xn"]), r(b["hh"]), s, s], rows))
-            ops.append(Op(dn_k, [s, r(w["down"]), r(b["hh"]), xr, s, s], rows))
+            ops += self.block_ops(x, start, rows, st, min(bk for bk in self.buckets if bk >= rows))
+        return ops
+
+    def block_ops(self, x, start, rows, st, m):
+        """The ops of one block (block_in): rows `start..start+rows` of x on
+        the kernels picked for bucket m; `st` holds state[3] = rows."""
+        h, b, w = self.h, self.buf, self.w
+        gu_k, sw_k, dn_k = self.kern[m]
+        xr = r(x, start * h * 2, rows * h * 2)
+        s = r(st)
+        ops = [Op(self.norm_k, [xr, r(w["post_norm"]), r(b["xn"])], rows)]
+        if sw_k >= 0:
+            ops.append(Op(gu_k, [s, r(w["gate_up"]), r(b["xn"]), r(b["gu"]), s, s], rows))
+            ops.append(Op(sw_k, [r(b["gu"]), r(b["hh"])], rows))
+        else:
+            ops.append(Op(gu_k, [s, r(w["gate_up"]), r(b["xn"]), r(b["hh"]), s, s], rows))
+        ops.append(Op(dn_k, [s, r(w["down"]), r(b["hh"]), xr, s, s], rows))
         return ops
 
     def states(self, n, chunk=None):
@@ -837,51 +893,28 @@ class PrefillMlp:
                 for _, rows in blocks_of(n, chunk or self.chunk)]
 
     def autotune_chunk(self, engine, seed=0x5EED00C0):
-        """autotune_chunk (qwen.rs:2962-3027) over this MLP half: a prompt of
-        prefill.block rows (seeded N(0,1) residual rows, the reference's
-        probe ids) cut by each of 1024, 2048, 4096, 8192 rows below
-        prefill.block and by prefill.block itself (blocks_of), the first
-        candidate run until auto.heat ms of GPU time have passed, then three
-        rounds in alternating order, the median of each; the fastest kept
-        as self.chunk and logged as the reference logs it."""
-        import time
-        t0 = time.time()
-        block = engine.tune_get("prefill.block")
-        cands = [c for c in (1024, 2048, 4096, 8192) if c < block] + [block]
-        if len(cands) < 2:
-            return self.chunk
-        g, n = self.gpu, block
+        """autotune_chunk (qwen.rs:2962-3027) over this MLP half, the policy
+        in the library (hb_engine_autotune_chunk): this side runs one block
+        of a prompt of prefill.block seeded N(0,1) residual rows (block_in)
+        and restores the rows a block adds into (reset).  The choice is kept
+        as self.chunk."""
+        g, n = self.gpu, engine.tune_get("prefill.block")
         x0 = normal_bf16(seed, 1.0, (n, self.h))
         X = g.alloc_with(x0)
-        plans = {}
+        states = {}
+
+        def block_in(start, rows):
+            if rows not in states:
+                states[rows] = g.alloc_with(np.array([0, 0, 0, rows], np.uint32))
+            m = min(bk for bk in self.buckets if bk >= rows)
+            return g.time_ops(self.block_ops(X, start, rows, states[rows], m), 1)
+
         try:
-            for c in cands:
-                st = self.states(n, c)
-                plans[c] = (st, self.ops(X, n, st, c))
-
-            def run(c):
-                g.upload(X, x0)  # reset: the block adds into x
-                return g.time_ops(plans[c][1], 1)
-
-            heat = engine.tune_get("auto.heat") * 1e-3
-            warmed = run(cands[0])
-            while warmed < heat:
-                warmed += run(cands[0])
-            times = {c: [] for c in cands}
-            for rnd in range(3):
-                for c in (cands if rnd % 2 == 0 else cands[::-1]):
-                    times[c].append(run(c))
-            med = {c: sorted(v)[1] for c, v in times.items()}
-            best = min(cands, key=lambda c: med[c])
-            self.chunk = best
-            engine.log_line("[autotune] blocks over %d rows, every layer, heated %.1f s, median of 3 rounds: %s -> %d"
-                            % (block, warmed, ", ".join("%d %.3f ms" % (c, med[c] * 1e3) for c in cands), best),
-                            time.time() - t0)
-            return best
+            self.chunk = autotune_chunk(engine, block_in, lambda: g.upload(X, x0))
+            return self.chunk
         finally:
-            for st, _ in plans.values():
-                for b in st:
-                    g.free(b)
+            for b in states.values():
+                g.free(b)
             g.free(X)
 
     def free(self):

@@ -175,12 +175,18 @@ typedef struct hb_desc {
      * fragments from LDS between its MFMAs (3 or 4 stages, an even count of
      * K tiles). */
     uint32_t sched;
-    /* MFMA GEMM (dense rows, direct-to-LDS, sched 0), 0 or 1 = no split: K
-     * cut into `ksplit` equal parts, one workgroup per (tile, part) writing
+    /* MFMA GEMM (dense rows, direct-to-LDS, any sched), 0 or 1 = no split:
+     * K cut into `ksplit` equal parts, one workgroup per (tile, part) writing
      * its f32 sums to a workspace the context owns, then a second kernel
      * adding the parts in order 0..ksplit-1 and applying Out -- for shapes
-     * whose tiles fill less than a round of the CUs.  One launch handle:
-     * hb_launch / hb_time run both kernels. */
+     * whose tiles fill less than a round of the CUs.  Each part must hold a
+     * whole number of K tiles (sched 3: an even number), and N must be a
+     * multiple of 4 (the second kernel's vector width).  One launch handle:
+     * hb_launch / hb_time run both kernels.  The workspace grows on the
+     * first launch over more rows than any before it on the context: that
+     * launch synchronizes the stream and calls hipFree / hipMalloc (not
+     * allowed under stream capture), so launch a split kernel once at its
+     * largest rows before capturing it. */
     uint32_t ksplit;
 } hb_desc;
 
@@ -221,7 +227,10 @@ double hb_compile_seconds(hb_gpu *gpu);
  *   COMBINE: y, route, out    ROUND_PROBE: state (state[0] = chunk), out_int, out_hw
  *   MOE_OUT: xn, shared_gate, experts, shared, x (x updated in place)
  *   RMSNORM: x, w, y (eps_bits, plus_one of the descriptor)
- * `m` is the rows of the block (the kernels read state[3], never beyond m). */
+ * `m` is the rows of the block (the kernels read state[3], never beyond m).
+ * A split-K GEMM (ksplit > 1) launched over more rows than any earlier
+ * split launch on this context first grows the context's workspace: the
+ * stream is synchronized and the workspace reallocated. */
 int hb_launch(hb_gpu *gpu, int32_t kernel, const hb_range *bindings, uint32_t nbind, uint32_t m);
 
 typedef struct hb_op { /* Op {pipe, ranges, groups} (qwen.rs:650-655) */
@@ -255,7 +264,9 @@ typedef struct hb_engine hb_engine;
 
 /* Tune::default + Tune::apply (qwen.rs:62-389) on `tune` ("key=value,..."),
  * over the context `gpu`.  HB_ERR_INVALID with the reference's message on a
- * bad key or value. */
+ * bad key or value.  `gpu` may be null: a host-only engine (the --tune
+ * table, the log, hb_engine_autotune_chunk over the host's callbacks) whose
+ * kernel selections (gemm, gate_up, matvec, experts) return HB_ERR_INVALID. */
 int hb_engine_open(hb_gpu *gpu, const char *tune, hb_engine **engine);
 void hb_engine_close(hb_engine *engine);
 /* Tune::summary (qwen.rs:391-398) of the settings this path reads. */
@@ -420,6 +431,30 @@ int hb_ckpt_upload(hb_gpu *gpu, hb_ckpt *ckpt, const char *const *keys, const ui
  * blocks of equal size rounded up to 64 rows (the last shorter); starts and
  * rows of up to `cap` blocks; returns the count. */
 uint32_t hb_blocks_of(uint32_t n, uint32_t chunk, uint32_t *starts, uint32_t *rows, uint32_t cap);
+
+/* The host's side of a prefill, for autotune_chunk: `block_in` runs the
+ * block of `rows` prompt rows starting at row `start` through every layer
+ * the host prefills (QwenEngine::block_in, qwen.rs:2637-2894) and returns
+ * its GPU seconds in *seconds; `reset` empties the conversation
+ * (QwenEngine::reset: here, whatever state a block updates in place, e.g.
+ * the residual stream, restored; may be null).  Both return 0 on success. */
+typedef struct hb_prefill_host {
+    void *ctx;
+    int (*block_in)(void *ctx, uint32_t start, uint32_t rows, double *seconds);
+    int (*reset)(void *ctx);
+} hb_prefill_host;
+
+/* autotune_chunk (qwen.rs:2962-3010): the rows per block for long prompts.
+ * Candidates 1024, 2048, 4096 and 8192 below prefill.block, and
+ * prefill.block; the first block of cands[0] rows run (after a reset) until
+ * auto.heat ms of GPU time have passed; then three rounds, the order
+ * reversed every other one, each a reset and a prompt of prefill.block rows
+ * cut by hb_blocks_of(prefill.block, candidate); the median of each
+ * candidate; the fastest into *chunk (prefill.block alone: no timing) and
+ * the line "[autotune] blocks over B rows, every layer, heated X s, median
+ * of 3 rounds: c t ms, ... -> best" logged.  HB_ERR_INVALID when a host
+ * callback fails. */
+int hb_engine_autotune_chunk(hb_engine *engine, const hb_prefill_host *host, uint32_t *chunk);
 
 /* Tune::default + Tune::apply + Tune::summary without a device: HB_OK and
  * the summary in `summary` (cap bytes), or HB_ERR_INVALID and the

@@ -208,7 +208,8 @@ def test_gemm_config2_layer_shapes(gpu, name, k, n, out, m):
     rows = np.unique(np.concatenate([[0, 1, m - 1], np.linspace(0, m - 1, 45).astype(int)]))
     want = orc.gemm(x[rows], w, out, None if y0 is None else y0[rows])
     acc = orc.gemm(x[rows], w, orc.OUT_F32) if out == 2 else None
-    check_close(got[rows], want, k, abs_products(x, w, rows), "%s m=%d" % (name, m), acc=acc)
+    check_close(got[rows], want, k, abs_products(x, w, rows), "%s m=%d" % (name, m), acc=acc,
+                min_exact=0.98)
 
 
 @pytest.mark.parametrize("name,k,n", [("qkv", 5120, 7168), ("gate_up", 5120, 34816),
@@ -220,7 +221,7 @@ def test_gemm_config4_27b_shapes(gpu, name, k, n):
     got = run_gemm(gpu, x, w, 0, **TILES["t256x256_w8_d4"])
     rows = np.array([0, 1, 517, 1024, 1500, 2000, 2046, 2047])
     want = orc.gemm(x[rows], w)
-    check_close(got[rows], want, k, abs_products(x, w, rows), name)
+    check_close(got[rows], want, k, abs_products(x, w, rows), name, min_exact=0.98)
 
 
 def test_gemm_full_size_properties(gpu):

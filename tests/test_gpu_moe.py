@@ -179,7 +179,7 @@ def test_grouped_gemm_gather_and_scatter(gpu, tname, bm):
     for e in np.unique(ex):
         sel = np.nonzero(ex == e)[0]
         ap[sel] = abs_products(x[lst[sel] // TOPK], wgu[e * 2 * MI:(e + 1) * 2 * MI])
-    check_close(got, want, H, ap, "gate_up " + tname)
+    check_close(got, want, H, ap, "gate_up " + tname, min_exact=0.98)
 
     xs = hb.normal_bf16(0x5EED0009, 1.0, (rows * TOPK, MI))
     wd = hb.normal_bf16(0x5EED000A, 0.02, (E * H, MI))
@@ -189,7 +189,7 @@ def test_grouped_gemm_gather_and_scatter(gpu, tname, bm):
     for e in np.unique(ex):
         sel = np.nonzero(ex == e)[0]
         ap[lst[sel]] = abs_products(xs[sel], wd[e * H:(e + 1) * H])
-    check_close(got, want, MI, ap, "down " + tname)
+    check_close(got, want, MI, ap, "down " + tname, min_exact=0.98)
 
 
 @pytest.mark.parametrize("bm,bn,wm,wn", [(32, 128, 1, 4), (128, 128, 2, 2), (64, 256, 1, 4)])

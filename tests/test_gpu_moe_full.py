@@ -92,7 +92,7 @@ def test_config5_layer_through_picks(gpu, tune):
             ap[sel] = abs_products(xr[sel], wr)
         if not layer.fused:
             egu = gpu.download(b["egu"], np.uint16, P * 2 * MI).reshape(P, 2 * MI)
-            check_close(egu, gu, H, ap, "grouped gate|up " + tune)
+            check_close(egu, gu, H, ap, "grouped gate|up " + tune, min_exact=0.98)
         g, u = (bf16_to_f32(gu[:, :MI]).astype(np.float64), bf16_to_f32(gu[:, MI:]).astype(np.float64))
         dg = 2 * bf16_ulp(g) + 2 * gamma(H) * ap[:, :MI]
         du = 2 * bf16_ulp(u) + 2 * gamma(H) * ap[:, MI:]
@@ -110,7 +110,7 @@ def test_config5_layer_through_picks(gpu, tune):
         for e_ in np.unique(ex):
             sel = np.nonzero(ex == e_)[0]
             apd[lst[sel]] = abs_products(ehb[sel], wdn[e_ * H:(e_ + 1) * H])
-        check_close(ey, want_ey, MI, apd, "grouped down " + tune)
+        check_close(ey, want_ey, MI, apd, "grouped down " + tune, min_exact=0.98)
 
         # moe_combine on the GPU's slot rows: bit for bit.
         assert np.array_equal(out, orc.combine(ey, route, TOPK, H))

@@ -46,11 +46,14 @@ def test_every_matvec_candidate_within_contract(gpu, name, k, n, out, m):
     try:
         cands = e.matvec_candidates(k, n, out, m)
         assert len(cands) >= 10
-        for d in cands:
+        for i, d in enumerate(cands):
             try:
                 kern = gpu.pipeline(d)
-            except hb.HerbertError:
-                continue  # not built for this shape: the selection skips it too
+            except hb.HerbertError as ex:
+                # only the emitter's refusals for this shape are skipped
+                assert i > 0 and ex.code in (hb.HB_ERR_UNSUPPORTED, hb.HB_ERR_INVALID), \
+                    "%s: candidate %d not built: %s" % (name, i, ex)
+                continue
             if y0 is not None:
                 gpu.upload(Y, y0)
             gpu.launch(kern, [hb.r(W), hb.r(X), hb.r(Y)], m)
@@ -58,7 +61,7 @@ def test_every_matvec_candidate_within_contract(gpu, name, k, n, out, m):
             got = gpu.download(Y, np.uint16, m * n).reshape(m, n)[:, sel]
             kn = gpu.kernel_name(kern)
             print("[mv picks] %s m=%d %s" % (name, m, kn), flush=True)
-            check_close(got, want, k, ap, "%s m=%d %s" % (name, m, kn), acc=acc)
+            check_close(got, want, k, ap, "%s m=%d %s" % (name, m, kn), acc=acc, min_exact=0.98)
             checked.append(kn)
     finally:
         e.close()
@@ -103,17 +106,19 @@ def test_every_fused_matvec_candidate_within_contract(gpu, name, k, n, out, m):
     try:
         cands = e.matvec_candidates(k, n, out, m, xsrc=hb.XSrc.Norm, eps=eps, plus_one=True)
         assert len(cands) >= 5
-        for d in cands:
+        for i, d in enumerate(cands):
             try:
                 kern = gpu.pipeline(d)
-            except hb.HerbertError:
+            except hb.HerbertError as ex:
+                assert i > 0 and ex.code in (hb.HB_ERR_UNSUPPORTED, hb.HB_ERR_INVALID), \
+                    "%s: candidate %d not built: %s" % (name, i, ex)
                 continue
             gpu.launch(kern, [hb.r(W), hb.r(X), hb.r(Y), hb.r(NW)], m)
             gpu.sync()
             got = gpu.download(Y, np.uint16, m * yn).reshape(m, yn)[:, sel]
             kn = gpu.kernel_name(kern)
             print("[mv picks] %s m=%d %s" % (name, m, kn), flush=True)
-            check_close(got, want, k, ap, "%s m=%d %s" % (name, m, kn), ulps=ulps)
+            check_close(got, want, k, ap, "%s m=%d %s" % (name, m, kn), ulps=ulps, min_exact=0.95)
             checked.append(kn)
     finally:
         e.close()

@@ -21,7 +21,10 @@ pytestmark = pytest.mark.gpu
 SHAPES = ([("config1", 512, 1024, 3584, 0)]
           + [("%s_m%d" % (nm, m), m, k, n, out) for m in (512, 1024, 2048)
              for nm, k, n, out in (("qkv", 2560, 4608, 0), ("o", 4096, 2560, 2),
-                                   ("gate_up", 2560, 18432, 0), ("down", 9216, 2560, 2))]
+                                   ("gate_up", 2560, 18432, 0), ("down", 9216, 2560, 2),
+                                   # the real Qwen3.5-4B fused [q+gate | k | v] width
+                                   # (qwen_kernels.rs:41-51, probe.rs:738-741)
+                                   ("qkv10240", 2560, 10240, 0))]
           + [("27b_%s" % nm, 2048, k, n, 0) for nm, k, n in (("qkv", 5120, 7168),
                                                               ("gate_up", 5120, 34816),
                                                               ("down", 17408, 5120),
@@ -46,11 +49,17 @@ def test_every_selection_candidate_within_contract(gpu, name, m, k, n, out):
     try:
         cands = e.gemm_candidates(k, n, out)
         assert len(cands) >= 30
-        for d in cands:
+        for i, d in enumerate(cands):
             try:
                 kern = gpu.pipeline(d)
-            except hb.HerbertError:
-                continue  # not built for this shape: the selection skips it too
+            except hb.HerbertError as ex:
+                # Only the emitter's refusals of a form for this shape (a K
+                # that does not split into whole tiles, an odd tile count) are
+                # skipped, as the selection skips them; a compile failure of a
+                # form the shape admits, or of the production kernel, fails.
+                assert i > 0 and ex.code in (hb.HB_ERR_UNSUPPORTED, hb.HB_ERR_INVALID), \
+                    "%s: candidate %d not built: %s" % (name, i, ex)
+                continue
             if y0 is not None:
                 gpu.upload(Y, y0)
             gpu.launch(kern, [hb.r(st), hb.r(W), hb.r(X), hb.r(Y), hb.r(st), hb.r(st)], m)
@@ -58,7 +67,7 @@ def test_every_selection_candidate_within_contract(gpu, name, m, k, n, out):
             got = gpu.download(Y, np.uint16, m * n).reshape(m, n)[rows]
             kn = gpu.kernel_name(kern)
             print("[picks] %s %s" % (name, kn), flush=True)
-            check_close(got, want, k, absprod, "%s %s" % (name, kn), acc=acc)
+            check_close(got, want, k, absprod, "%s %s" % (name, kn), acc=acc, min_exact=0.98)
             checked.append(kn)
     finally:
         e.close()
