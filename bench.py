@@ -73,6 +73,30 @@ MARK_BYTES = 7 * 4096  # the trace marker fill: 7 workgroups of 256 threads
 HEAT_S = 1.0
 
 
+# Named regions of the run: each timed region is bracketed by two marker
+# fills (a dispatch of MARK_BYTES / 16 threads that a kernel trace or a
+# counter run tells apart by its grid), and its name appended here in the
+# order the regions ran; the JSON line carries the list ("regions"), so the
+# trace and counter summaries attribute each dispatch to its case.
+REGIONS = []
+_MARK = {}
+
+
+class region:
+    def __init__(self, g, name):
+        self.g, self.name = g, name
+
+    def __enter__(self):
+        if self.g not in _MARK:
+            _MARK[self.g] = self.g.alloc(MARK_BYTES)
+        self.g.zero(_MARK[self.g])
+        return self
+
+    def __exit__(self, *a):
+        self.g.zero(_MARK[self.g])
+        REGIONS.append(self.name)
+
+
 def heat(g, ops, seconds=None):
     """The ops run back to back, ~50 ms a submission, until `seconds` (HEAT_S
     by default) of GPU time have passed (untimed)."""
@@ -227,12 +251,19 @@ def main():
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--traffic-run", action="store_true")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
+    ap.add_argument("--counter-run", action="store_true",
+                    help="the bench's regions with --heat 0 and then the calibration copy, for rocprofv3 --pmc")
+    ap.add_argument("--counter-summary", nargs="+", metavar="BENCH_OUT CSV",
+                    help="that run's stdout, then one counter_collection.csv per counter pass")
     ap.add_argument("--trace-summary", nargs=3, metavar=("TRACE_CSV", "BENCH_OUT", "COMMAND"))
     ap.add_argument("--yardstick", action="store_true",
                     help="time hipBLASLt (torch.matmul) on the step's shapes instead")
     args = ap.parse_args()
     if args.traffic_summary:
         traffic_summary(*args.traffic_summary)
+        return
+    if args.counter_summary:
+        counter_summary(args.counter_summary[0], args.counter_summary[1:])
         return
     if args.trace_summary:
         trace_summary(*args.trace_summary)
@@ -245,7 +276,7 @@ def main():
               "each GEMM by N across GPUs, which is not built" % args.gpus, file=sys.stderr)
         sys.exit(2)
 
-    HEAT_S = max(0.0, args.heat)
+    HEAT_S = 0.0 if args.counter_run else max(0.0, args.heat)
     import herbert_hip as hb
     g = hb.Gpu(0)
     log("[gpu]", g.summary())
@@ -276,10 +307,11 @@ def main():
     g.time_ops(ops, max(args.warmup, 0)) if args.warmup > 0 else None
     heat(g, ops)
     g.sync()
-    t = g.time_ops(ops, args.steps)
-    g.sync()
-    t_ev, each = g.time_each(ops, args.steps)
-    g.sync()
+    with region(g, "step_m2048"):
+        t = g.time_ops(ops, args.steps)
+        g.sync()
+        t_ev, each = g.time_each(ops, args.steps)
+        g.sync()
     ms = t / args.steps * 1e3
     value = flops / (t / args.steps) / 1e12
 
@@ -323,23 +355,32 @@ def main():
     if not args.no_moe:
         result["moe"] = bench_moe(g, e, hb)
     e.log_summary()
+    if args.counter_run:
+        counter_run(g, hb)
     e.close()
     g.close()
-    if not args.no_cpu:
+    if not args.no_cpu and not args.counter_run:
         result["cpu_baseline"] = cpu_baseline(args.cpu_rows)
+    result["regions"] = REGIONS
     print(json.dumps(result), flush=True)
 
 
-def traffic_of(kernel):
-    """The kernel's HBM bytes per launch from profiles/traffic.json (FETCH_SIZE
-    + WRITE_SIZE of its full-block dispatches, scaled), or None."""
+def traffic_of(kernel, where="step_m2048"):
+    """The kernel's HBM bytes per launch in region `where` from
+    profiles/counters.json (FETCH_SIZE + WRITE_SIZE of its full-size
+    dispatches, scaled), else from profiles/traffic.json, or None."""
+    path = os.path.join(ROOT, "profiles", "counters.json")
+    if os.path.exists(path):
+        c = json.load(open(path)).get(where, {}).get(kernel)
+        if c and "bytes" in c:
+            return {"bytes": c["bytes"], "fetch_bytes": c["fetch_bytes"], "write_bytes": c["write_bytes"]}
     path = os.path.join(ROOT, "profiles", "traffic.json")
     if not os.path.exists(path):
         return None
     return json.load(open(path)).get(kernel)
 
 
-def gemm_set(g, e, hb, shapes, m, steps, seed):
+def gemm_set(g, e, hb, shapes, m, steps, seed, tag):
     """The GEMMs `shapes` [(name, K, N, out)] over m rows, each on the kernel
     the selection layer picks, run back to back: the set's TFLOP/s and each
     GEMM's (launch-event) time."""
@@ -353,16 +394,11 @@ def gemm_set(g, e, hb, shapes, m, steps, seed):
         kern = e.gemm(k, n, out, hb.r(state), hb.r(W), hb.r(X), hb.r(Y), m)
         ops.append(hb.Op(kern, [hb.r(state), hb.r(W), hb.r(X), hb.r(Y), hb.r(state), hb.r(state)], m))
         flops.append(2.0 * m * n * k)
-    # Trace markers around the timed region (a fill of MARK_BYTES: its
-    # dispatch's grid tells it apart in a kernel trace).
-    mark = g.alloc(MARK_BYTES)
-    bufs.append(mark)
     g.time_ops(ops, 2)
     heat(g, ops)
-    g.zero(mark)
-    t = g.time_ops(ops, steps)
-    _, each = g.time_each(ops, steps)
-    g.zero(mark)
+    with region(g, tag):
+        t = g.time_ops(ops, steps)
+        _, each = g.time_each(ops, steps)
     g.sync()
     out = {"m": m, "tflops": round(sum(flops) / (t / steps) / 1e12, 1),
            "frac": round(sum(flops) / (t / steps) / 1e12 / MFMA_BF16_PEAK, 4),
@@ -381,24 +417,24 @@ def bench_prefill_more(g, e, hb, steps):
     config 4 (27B-class shapes at M=2048, lm_head included), and the
     reference's real 4B fused QKV (2560 -> 10240) at M=512, 1024, 2048."""
     steps = max(3, min(steps, 10))
-    res = {"config1": gemm_set(g, e, hb, CONFIG1, 512, steps, 0x5EED0001)}
+    res = {"config1": gemm_set(g, e, hb, CONFIG1, 512, steps, 0x5EED0001, "config1")}
     # config 1's kernel name is its own (no other case has 1024 x 3584), so
     # its traffic counters are config 1's: HBM bytes per launch against the
     # algorithmic 2*(M*K + N*K + M*N).
     c1 = res["config1"]["gemms"]["gemm"]
-    tr = traffic_of(c1["kernel"])
+    tr = traffic_of(c1["kernel"], "config1")
     k, n = CONFIG1[0][1], CONFIG1[0][2]
     c1["algorithmic_bytes"] = 2 * (512 * k + n * k + 512 * n)
     c1["traffic"] = tr["bytes"] if tr else None
     for m in (512, 1024):
-        res["config2_m%d" % m] = gemm_set(g, e, hb, LAYER, m, steps, SEED)
+        res["config2_m%d" % m] = gemm_set(g, e, hb, LAYER, m, steps, SEED, "config2_m%d" % m)
     # The reference's real Qwen3.5-4B fused QKV width: q_width = 2 * heads *
     # head_dim carries the output gate, 8192 + 2 * 1024 = 10240 columns
     # (qwen_kernels.rs:41-51, probe.rs:738-741), where BASELINE's config 2
     # names 2560 + 2 * 1024: reported beside it, at each block size.
     for m in (512, 1024, 2048):
-        res["qkv10240_m%d" % m] = gemm_set(g, e, hb, QKV_REAL, m, steps, SEED + 40)
-    res["config4_m2048"] = gemm_set(g, e, hb, CONFIG4, M, steps, 0x5EED0004)
+        res["qkv10240_m%d" % m] = gemm_set(g, e, hb, QKV_REAL, m, steps, SEED + 40, "qkv10240_m%d" % m)
+    res["config4_m2048"] = gemm_set(g, e, hb, CONFIG4, M, steps, 0x5EED0004, "config4_m2048")
     return res
 
 
@@ -409,7 +445,7 @@ def traffic_run(g, e, ops, per_gemm):
     import herbert_hip as hb
     g.time_ops(ops, 3)
     g.sync()
-    c1 = gemm_set(g, e, hb, CONFIG1, 512, 3, 0x5EED0001)
+    c1 = gemm_set(g, e, hb, CONFIG1, 512, 3, 0x5EED0001, "config1")
     g.sync()
     a, b = g.alloc(COPY_BYTES), g.alloc(COPY_BYTES)
     g.zero(a)
@@ -420,6 +456,108 @@ def traffic_run(g, e, ops, per_gemm):
     g.free(b)
     print(json.dumps({"picked": {nm: d["kernel"] for nm, d in per_gemm.items()},
                       "config1": c1["gemms"]["gemm"]["kernel"], "copy_bytes": COPY_BYTES}), flush=True)
+
+
+def counter_run(g, hb):
+    """After the bench's regions (run with --counter-run: heat 0, few
+    steps), the calibration copy in a region of its own: COPY_BYTES read
+    and COPY_BYTES written by HIP's blit kernel."""
+    a, b = g.alloc(COPY_BYTES), g.alloc(COPY_BYTES)
+    g.zero(a)
+    g.sync()
+    with region(g, "calibration"):
+        for _ in range(5):
+            g.copy(hb.r(b), hb.r(a))
+    g.sync()
+    g.free(a)
+    g.free(b)
+
+
+# Derived columns of the counter summary: FETCH_SIZE / WRITE_SIZE scaled by
+# what they read for the calibration copy; the L2 hit rate; the MFMA pipes'
+# busy cycles per SIMD (1024 SIMDs), as microseconds at 2.4 GHz, to set
+# beside the kernel's own duration.
+SIMDS, CLOCK_MHZ = 1024, 2400.0
+
+
+def counter_summary(bench_out, csvs):
+    """profiles/counters.json and profiles/counters_summary.txt from
+    `rocprofv3 --pmc ... --output-format csv` runs of `bench.py
+    --counter-run` (one per counter pass) and that run's stdout: each
+    dispatch attributed to the region it ran in (between the marker fills,
+    named by the JSON line's "regions"), then per region and kernel the
+    median of each counter over its full-size dispatches."""
+    import csv
+    import statistics
+    b = None
+    for ln in open(bench_out):
+        if ln.startswith("{") and '"regions"' in ln:
+            b = json.loads(ln)
+    if b is None:
+        sys.exit("counter summary: no JSON line with regions in %s" % bench_out)
+    names = b["regions"]
+    acc = {}
+    for path in csvs:
+        disp = {}
+        for r in csv.DictReader(open(path)):
+            d = disp.setdefault(int(r["Dispatch_Id"]), {"k": r["Kernel_Name"], "grid": int(r["Grid_Size"]), "c": {}})
+            d["c"][r["Counter_Name"]] = d["c"].get(r["Counter_Name"], 0.0) + float(r["Counter_Value"])
+        seq = [disp[i] for i in sorted(disp)]
+        marks = [i for i, d in enumerate(seq) if d["k"].startswith("fill_zero") and d["grid"] == MARK_BYTES // 16]
+        if len(marks) != 2 * len(names):
+            sys.exit("counter summary: %s holds %d markers for %d regions" % (path, len(marks), len(names)))
+        for ri, nm in enumerate(names):
+            for d in seq[marks[2 * ri] + 1:marks[2 * ri + 1]]:
+                acc.setdefault(nm, {}).setdefault(d["k"], []).append((d["grid"], d["c"]))
+    out = {}
+    for nm, kern in acc.items():
+        for k, v in kern.items():
+            top = max(gs for gs, _ in v)
+            full = [c for gs, c in v if gs == top]
+            cnames = sorted({cn for c in full for cn in c})
+            out.setdefault(nm, {})[k] = {"dispatches": len(full), "grid": top}
+            out[nm][k].update({cn: statistics.median(c[cn] for c in full if cn in c) for cn in cnames})
+    cal = out.get("calibration", {})
+    copy = next((v for k, v in cal.items() if "copyBuffer" in k), None)
+    if not copy or "FETCH_SIZE" not in copy or "WRITE_SIZE" not in copy:
+        sys.exit("counter summary: no calibration copy with FETCH_SIZE and WRITE_SIZE")
+    kib = COPY_BYTES / 1024.0
+    sf, sw = kib / copy["FETCH_SIZE"], kib / copy["WRITE_SIZE"]
+    for nm, kern in out.items():
+        for k, c in kern.items():
+            if "FETCH_SIZE" in c:
+                c["fetch_bytes"] = round(c["FETCH_SIZE"] * sf * 1024.0)
+            if "WRITE_SIZE" in c:
+                c["write_bytes"] = round(c["WRITE_SIZE"] * sw * 1024.0)
+            if "fetch_bytes" in c and "write_bytes" in c:
+                c["bytes"] = c["fetch_bytes"] + c["write_bytes"]
+            if c.get("TCC_HIT_sum", 0) + c.get("TCC_MISS_sum", 0) > 0:
+                c["l2_hit_rate"] = round(c["TCC_HIT_sum"] / (c["TCC_HIT_sum"] + c["TCC_MISS_sum"]), 4)
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in c:
+                c["mfma_busy_us_per_simd"] = round(c["SQ_VALU_MFMA_BUSY_CYCLES"] / SIMDS / CLOCK_MHZ, 3)
+    out["_calibration"] = {"copy_bytes": COPY_BYTES, "fetch_scale": round(sf, 4), "write_scale": round(sw, 4),
+                           "simds": SIMDS, "clock_mhz": CLOCK_MHZ}
+    path = os.path.join(ROOT, "profiles", "counters.json")
+    with open(path, "w") as fh:
+        json.dump(out, fh, indent=1, sort_keys=True)
+    lines = ["per region and kernel, medians over its full-size dispatches (bytes scaled by the calibration "
+             "copy: fetch x%.4f, write x%.4f); mfma_us = SQ_VALU_MFMA_BUSY_CYCLES / %d SIMDs / %.0f MHz"
+             % (sf, sw, SIMDS, CLOCK_MHZ), ""]
+    for nm in names:
+        if nm == "calibration" or nm not in out:
+            continue
+        lines.append(nm)
+        for k, c in sorted(out[nm].items()):
+            if k.startswith("fill_zero"):
+                continue
+            f = lambda key, sc=1.0, fmt="%.1f": (fmt % (c[key] * sc)) if key in c else "-"  # noqa: E731
+            lines.append("  %-72s fetch %8s MB write %7s MB l2hit %6s mfma_us %7s wait_any %10s mfma_insts %10s"
+                         % (k[:72], f("fetch_bytes", 1e-6), f("write_bytes", 1e-6), f("l2_hit_rate", 1.0, "%.3f"),
+                            f("mfma_busy_us_per_simd", 1.0, "%.2f"), f("SQ_WAIT_INST_ANY", 1.0, "%.0f"),
+                            f("SQ_INSTS_MFMA", 1.0, "%.0f")))
+    with open(os.path.join(ROOT, "profiles", "counters_summary.txt"), "w") as fh:
+        fh.write("\n".join(lines) + "\n")
+    print("wrote %s and counters_summary.txt: %d regions" % (path, len(out) - 1))
 
 
 def trace_summary(trace_csv, bench_json, cmd):
@@ -488,8 +626,10 @@ def trace_summary(trace_csv, bench_json, cmd):
         marks = [i for i, r in enumerate(rows) if r["Kernel_Name"] == "fill_zero"
                  and int(r.get("Grid_Size_X", r.get("Grid_Size", 0))) == MARK_BYTES // 16]
         regions = [rows[marks[2 * i] + 1:marks[2 * i + 1]] for i in range(len(marks) // 2)]
-        for ci, (case, st) in enumerate(pm.items()):
-            reg = regions[ci] if ci < len(regions) else []
+        names_r = b.get("regions") or list(pm)
+        for case, st in pm.items():
+            ci = names_r.index(case) if case in names_r else -1
+            reg = regions[ci] if 0 <= ci < len(regions) else []
             out.append("  %s: %.1f TFLOP/s (%.1f%% of 2.5 PFLOP/s), %.2f us a set; rocprof first-start..last-end "
                        "%.2f us a set" % (case, st["tflops"], 100 * st["frac"], st["us"],
                                           (int(reg[-1]["End_Timestamp"]) - int(reg[0]["Start_Timestamp"])) / 1e3
@@ -584,7 +724,8 @@ def bench_moe(g, e, hb):
     g.time_ops(ops, 3)
     heat(g, ops)
     reps = 20
-    t, each = g.time_each(ops, reps)
+    with region(g, "moe_layer"):
+        t, each = g.time_each(ops, reps)
     route = g.download(layer.buf["route"], np.uint32, T * 2 * TOPK).reshape(T, 2 * TOPK)
     used = len(np.unique(route[:, :TOPK]))
     P = T * TOPK
@@ -737,10 +878,26 @@ def bench_matvec(g, e, hb):
         g.time_ops(ops, 3)
         heat(g, ops)
         reps = 20
-        t = g.time_ops(ops, reps) / reps
-        gbs = nbytes / t / 1e9
-        r = {"value": round(gbs, 1), "unit": "GB/s", "frac": round(gbs / HBM_PEAK, 4), "peak": HBM_PEAK,
-             "ms_per_step": round(t * 1e3, 4), "m": mv_m, "layers": DECODE_LAYERS,
+        with region(g, "decode_m%d" % mv_m):
+            t = g.time_ops(ops, reps) / reps
+        # The same step recorded as one HIP graph (the reference encodes a
+        # step's ops in one command buffer, qwen.rs:3177), timed the same way.
+        gr = g.graph(ops)
+        try:
+            gr.time(3)
+            heat(g, ops)
+            gr.time(50)
+            tg = gr.time(reps) / reps
+        finally:
+            gr.free()
+        gbs, gbs_g = nbytes / t / 1e9, nbytes / tg / 1e9
+        best_gbs = max(gbs, gbs_g)
+        r = {"value": round(best_gbs, 1), "unit": "GB/s", "frac": round(best_gbs / HBM_PEAK, 4), "peak": HBM_PEAK,
+             "form": "graph" if gbs_g > gbs else "stream",
+             "stream": {"ms_per_step": round(t * 1e3, 4), "gbs": round(gbs, 1), "frac": round(gbs / HBM_PEAK, 4)},
+             "graph": {"ms_per_step": round(tg * 1e3, 4), "gbs": round(gbs_g, 1),
+                       "frac": round(gbs_g / HBM_PEAK, 4)},
+             "ms_per_step": round(min(t, tg) * 1e3, 4), "m": mv_m, "layers": DECODE_LAYERS,
              "bytes_per_step": nbytes, "kernels": {nm: g.kernel_name(kern[nm]) for nm in kern}}
         if mv_m == 1:
             # the lm_head alone, two copies in turn (2 x 778 MB: no copy is
@@ -762,8 +919,9 @@ def bench_matvec(g, e, hb):
         g.free(b)
     out = res[1]
     out["fused"] = res["fused"]
-    out["m4"] = {kk: res[4][kk] for kk in ("value", "frac", "ms_per_step", "kernels")}
-    out["m8"] = {kk: res[8][kk] for kk in ("value", "frac", "ms_per_step", "kernels")}
+    keys = ("value", "frac", "form", "stream", "graph", "ms_per_step", "kernels")
+    out["m4"] = {kk: res[4][kk] for kk in keys}
+    out["m8"] = {kk: res[8][kk] for kk in keys}
     return out
 
 

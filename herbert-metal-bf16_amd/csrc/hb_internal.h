@@ -94,6 +94,9 @@ struct hb_gpu {
     // grown before a launch that needs more, freed at hb_close.
     void* ws = nullptr;
     uint64_t ws_bytes = 0;
+    // Recorded graphs alive on this context: they hold the workspace's
+    // address, so it may not be reallocated meanwhile.
+    int graphs_live = 0;
 };
 
 namespace hb {

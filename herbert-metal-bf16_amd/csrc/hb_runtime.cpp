@@ -214,6 +214,9 @@ static int load_kernel(hb_gpu* g, const hb_desc& d, Kernel* k) {
 // launch in flight may still read the old one).
 static int ensure_ws(hb_gpu* g, uint64_t bytes) {
     if (bytes <= g->ws_bytes) return HB_OK;
+    if (g->graphs_live)
+        return fail(HB_ERR_INVALID, "the split-K workspace cannot grow while a recorded graph holds its "
+                                    "address (free the graphs first, or record after the largest launch)");
     HB_HIP(hipSetDevice(g->device));
     HB_HIP(hipStreamSynchronize(g->stream));
     if (g->ws) HB_HIP(hipFree(g->ws));
@@ -524,15 +527,20 @@ int hb_time(hb_gpu* g, const hb_op* ops, uint32_t nops, uint32_t reps, double* s
     return hb_time_each(g, ops, nops, reps, seconds, nullptr);
 }
 
-int hb_time_each(hb_gpu* g, const hb_op* ops, uint32_t nops, uint32_t reps, double* seconds,
-                 double* op_seconds) {
-    // Check every op once, then launch without re-checking.
-    struct Ready {
-        const Kernel* k;
-        void* ptrs[10];
-        uint32_t n, m, groups;
-    };
-    std::vector<Ready> ready(nops);
+}  // extern "C"
+
+namespace hb {
+// Ops checked once and resolved to what a launch needs (the split-K
+// workspace sized for them), so they can be launched without re-checking.
+struct Ready {
+    const Kernel* k;
+    void* ptrs[10];
+    uint32_t n, m, groups;
+};
+
+static int prepare(hb_gpu* g, const hb_op* ops, uint32_t nops, std::vector<Ready>* out) {
+    std::vector<Ready>& ready = *out;
+    ready.resize(nops);
     for (uint32_t i = 0; i < nops; i++) {
         const hb_op& op = ops[i];
         if (op.kernel < 0 || (size_t)op.kernel >= g->kernels.size())
@@ -555,6 +563,17 @@ int hb_time_each(hb_gpu* g, const hb_op* ops, uint32_t nops, uint32_t reps, doub
         ready[i].m = op.m;
         ready[i].groups = groups_of(k.desc, op.m);
     }
+    return HB_OK;
+}
+}  // namespace hb
+
+extern "C" {
+
+int hb_time_each(hb_gpu* g, const hb_op* ops, uint32_t nops, uint32_t reps, double* seconds,
+                 double* op_seconds) {
+    std::vector<Ready> ready;
+    int prc = prepare(g, ops, nops, &ready);
+    if (prc) return prc;
     if (!op_seconds) {
         HB_HIP(hipEventRecord(g->ev0, g->stream));
         for (uint32_t r = 0; r < reps; r++)
@@ -604,6 +623,71 @@ int hb_time_each(hb_gpu* g, const hb_op* ops, uint32_t nops, uint32_t reps, doub
     for (auto& e : ev)
         if (e) hipEventDestroy(e);
     return rc;
+}
+
+// A recorded op sequence: the ops captured from the context's stream into a
+// HIP graph (kernel nodes only: nothing here records a memset) and
+// instantiated once, then replayed with one launch per run.
+struct hb_graph {
+    hb_gpu* g = nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+int hb_graph_record(hb_gpu* g, const hb_op* ops, uint32_t nops, hb_graph** out) {
+    *out = nullptr;
+    if (!nops) return fail(HB_ERR_INVALID, "hb_graph_record: no ops");
+    std::vector<Ready> ready;
+    int rc = prepare(g, ops, nops, &ready);  // sizes the split-K workspace before the capture
+    if (rc) return rc;
+    HB_HIP(hipSetDevice(g->device));
+    HB_HIP(hipStreamBeginCapture(g->stream, hipStreamCaptureModeThreadLocal));
+    for (auto& x : ready)
+        if ((rc = launch_raw(g, *x.k, x.ptrs, x.n, x.m, x.groups))) break;
+    hipGraph_t graph = nullptr;
+    hipError_t he = hipStreamEndCapture(g->stream, &graph);
+    if (rc || he != hipSuccess) {
+        if (graph) hipGraphDestroy(graph);
+        return rc ? rc : hip_fail(he, "hipStreamEndCapture");
+    }
+    hipGraphExec_t exec = nullptr;
+    if ((he = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0)) != hipSuccess) {
+        hipGraphDestroy(graph);
+        return hip_fail(he, "hipGraphInstantiate");
+    }
+    hb_graph* r = new hb_graph();
+    r->g = g;
+    r->graph = graph;
+    r->exec = exec;
+    g->graphs_live++;
+    *out = r;
+    return HB_OK;
+}
+
+int hb_graph_launch(hb_graph* gr, uint32_t reps) {
+    for (uint32_t i = 0; i < reps; i++) HB_HIP(hipGraphLaunch(gr->exec, gr->g->stream));
+    return HB_OK;
+}
+
+int hb_graph_time(hb_graph* gr, uint32_t reps, double* seconds) {
+    hb_gpu* g = gr->g;
+    HB_HIP(hipEventRecord(g->ev0, g->stream));
+    for (uint32_t i = 0; i < reps; i++) HB_HIP(hipGraphLaunch(gr->exec, g->stream));
+    HB_HIP(hipEventRecord(g->ev1, g->stream));
+    HB_HIP(hipEventSynchronize(g->ev1));
+    float ms = 0;
+    HB_HIP(hipEventElapsedTime(&ms, g->ev0, g->ev1));
+    *seconds = ms * 1e-3;
+    return HB_OK;
+}
+
+void hb_graph_free(hb_graph* gr) {
+    if (!gr) return;
+    hipStreamSynchronize(gr->g->stream);
+    if (gr->exec) hipGraphExecDestroy(gr->exec);
+    if (gr->graph) hipGraphDestroy(gr->graph);
+    gr->g->graphs_live--;
+    delete gr;
 }
 
 int hb_sync(hb_gpu* g) {

@@ -397,6 +397,13 @@ class Gpu:
         check(lib.hb_time(self.h, arr, len(ops), int(reps), ctypes.byref(s)))
         return s.value
 
+    def graph(self, ops):
+        """The ops recorded into a HIP graph (hb_graph_record): a Graph."""
+        arr = (Op * len(ops))(*ops)
+        h = _P()
+        check(lib.hb_graph_record(self.h, arr, len(ops), ctypes.byref(h)))
+        return Graph(h)
+
     def time_each(self, ops, reps=1):
         """(GPU seconds of `reps` runs of `ops`, mean seconds of each op), one
         event after every launch on the library's stream."""
@@ -428,6 +435,33 @@ def tune_check(tune):
     buf = ctypes.create_string_buffer(8192)
     check(lib.hb_tune_check(tune.encode(), buf, len(buf)))
     return buf.value.decode()
+
+
+lib.hb_graph_record.argtypes = [_P, ctypes.POINTER(Op), _u32, ctypes.POINTER(_P)]
+lib.hb_graph_launch.argtypes = [_P, _u32]
+lib.hb_graph_time.argtypes = [_P, _u32, ctypes.POINTER(ctypes.c_double)]
+lib.hb_graph_free.argtypes = [_P]
+lib.hb_graph_free.restype = None
+
+
+class Graph:
+    """A recorded op sequence (hb_graph): replays with one launch each."""
+
+    def __init__(self, h):
+        self.h = h
+
+    def launch(self, reps=1):
+        check(lib.hb_graph_launch(self.h, int(reps)))
+
+    def time(self, reps=1):
+        s = ctypes.c_double()
+        check(lib.hb_graph_time(self.h, int(reps), ctypes.byref(s)))
+        return s.value
+
+    def free(self):
+        if self.h:
+            lib.hb_graph_free(self.h)
+            self.h = None
 
 
 class Engine:

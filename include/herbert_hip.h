@@ -250,6 +250,22 @@ int hb_time(hb_gpu *gpu, const hb_op *ops, uint32_t nops, uint32_t reps, double 
  * *seconds the whole run. */
 int hb_time_each(hb_gpu *gpu, const hb_op *ops, uint32_t nops, uint32_t reps, double *seconds,
                  double *op_seconds);
+
+/* A recorded op sequence: the reference encodes a decode step's ops into one
+ * command buffer and submits it (QwenEngine::step, qwen.rs:3177); here the
+ * ops are captured from the context's stream into a HIP graph (kernel nodes
+ * only, no memset nodes) and instantiated once, checked as hb_time checks
+ * them.  The bindings are fixed at record time (the buffers' contents may
+ * change between replays).  While a graph lives, the context's split-K
+ * workspace cannot grow (a launch that would need it to returns
+ * HB_ERR_INVALID). */
+typedef struct hb_graph hb_graph;
+int hb_graph_record(hb_gpu *gpu, const hb_op *ops, uint32_t nops, hb_graph **graph);
+/* `reps` replays on the context's stream (asynchronous, as hb_launch). */
+int hb_graph_launch(hb_graph *graph, uint32_t reps);
+/* GPU seconds of `reps` replays, events at the ends only. */
+int hb_graph_time(hb_graph *graph, uint32_t reps, double *seconds);
+void hb_graph_free(hb_graph *graph);
 /* submit_wait (metal/gpu.rs:209-221): wait for the stream. */
 int hb_sync(hb_gpu *gpu);
 
