@@ -71,6 +71,7 @@ MARK_BYTES = 7 * 4096  # the trace marker fill: 7 workgroups of 256 threads
 # 355-359 us after 1-15 s of load (the clocks ramp up under load); without a
 # heat, K=20 steps (8 ms) are timed mostly before the ramp.
 HEAT_S = 1.0
+COUNTER_RUN = False
 
 
 # Named regions of the run: each timed region is bracketed by two marker
@@ -236,7 +237,7 @@ def yardstick(steps):
 
 
 def main():
-    global HEAT_S
+    global HEAT_S, COUNTER_RUN
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
@@ -253,6 +254,9 @@ def main():
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     ap.add_argument("--counter-run", action="store_true",
                     help="the bench's regions with --heat 0 and then the calibration copy, for rocprofv3 --pmc")
+    ap.add_argument("--picks-out", metavar="FILE", help="write the engine's choices (hb_engine_picks) to FILE")
+    ap.add_argument("--picks-in", metavar="FILE",
+                    help="seed the engine's choices from FILE (hb_engine_pin): the same kernels as that run")
     ap.add_argument("--counter-summary", nargs="+", metavar="BENCH_OUT CSV",
                     help="that run's stdout, then one counter_collection.csv per counter pass")
     ap.add_argument("--trace-summary", nargs=3, metavar=("TRACE_CSV", "BENCH_OUT", "COMMAND"))
@@ -277,10 +281,13 @@ def main():
         sys.exit(2)
 
     HEAT_S = 0.0 if args.counter_run else max(0.0, args.heat)
+    COUNTER_RUN = args.counter_run
     import herbert_hip as hb
     g = hb.Gpu(0)
     log("[gpu]", g.summary())
     e = hb.Engine(g, args.tune)
+    if args.picks_in:
+        e.pin(open(args.picks_in).read())
     state = g.alloc_with(np.array([0, 0, 0, M], np.uint32))
     bufs, ops, flops, per_gemm = [], [], 0.0, {}
     t0 = time.time()
@@ -355,6 +362,9 @@ def main():
     if not args.no_moe:
         result["moe"] = bench_moe(g, e, hb)
     e.log_summary()
+    if args.picks_out:
+        with open(args.picks_out, "w") as fh:
+            fh.write(e.picks())
     if args.counter_run:
         counter_run(g, hb)
     e.close()
@@ -754,6 +764,10 @@ def bench_moe(g, e, hb):
     # publishes the reference's layer rate per tile size): the layer on
     # each, the rest of its selection timed as above.
     out["tiles"] = {}
+    if COUNTER_RUN:  # the counter passes cover the layer above, on pinned picks
+        g.free(wgu)
+        g.free(wdn)
+        return out
     for bm in (16, 32, 64):
         with hb.Engine(g, "moe.tile=%d" % bm) as et:
             lt = hb.MoeLayer(g, et, E, TOPK, H, MI, T, wgu, wdn, scores=hb.normal_bf16(seed, 1.0, (T, E)),

@@ -49,6 +49,10 @@ CHECKS = {
         "-DHB_K=2560 -DHB_N=18432 -DHB_OUT=0 -DHB_BM=256 -DHB_BN=288 -DHB_BK=32 -DHB_WM=2 -DHB_WN=2 "
         "-DHB_MFMA=16 -DHB_STAGES=4 -DHB_SWZ=2 -DHB_ORDER=1 -DHB_MFIRST=1 -DHB_BAND=4 -DHB_SCHED=3",
     ],
+    "mv_chain.hip": ["-DHB_MV_M=4 -DHB_NPH=5 -DHB_PH_K=2560,4096,2560,9216,2560 "
+                     "-DHB_PH_N=4608,2560,18432,2560,151936 -DHB_PH_OUT=0,2,0,2,0 -DHB_CPL=18",
+                     "-DHB_MV_M=8 -DHB_NPH=3 -DHB_PH_K=512,1536,1024 -DHB_PH_N=1536,1024,700 "
+                     "-DHB_PH_OUT=0,2,1 -DHB_CPL=3"],
     "fill.hip": [""],
     "probe.hip": [""],
     "gemm_simt.hip": ["-DHB_K=2560 -DHB_N=4608 -DHB_OUT=2 -DHB_MFIRST=1"],

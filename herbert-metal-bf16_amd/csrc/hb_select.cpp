@@ -400,6 +400,11 @@ struct hb_engine {
     std::map<std::string, int32_t> gemm_pick;
     std::map<std::string, std::pair<int32_t, int32_t>> gate_up_pick;
     std::map<std::string, hb_desc> mv_pick;
+    struct ExpertsPick {
+        int32_t kernels[4];
+        uint32_t bm;
+    };
+    std::map<std::string, ExpertsPick> experts_pick;
     std::vector<std::pair<std::string, hb_desc>> extra;  // hb_engine_add_gemm_candidate
     double autotune_seconds = 0.0;
     bool timed = false;
@@ -1144,6 +1149,14 @@ int hb_engine_experts(hb_engine* e, uint32_t experts, uint32_t top_k, uint32_t h
         *bm_out = bm;
         return HB_OK;
     }
+    char ekey[96];
+    snprintf(ekey, sizeof ekey, "%u %u %u %u, %u rows", experts, top_k, hidden, inter, m);
+    auto eit = e->experts_pick.find(ekey);
+    if (eit != e->experts_pick.end()) {
+        for (int i = 0; i < 4; i++) kernels[i] = eit->second.kernels[i];
+        *bm_out = eit->second.bm;
+        return HB_OK;
+    }
     // swiglu_slots after an unfused gate|up (EGU -> EHB), timed with it.
     hb_desc swd{};
     swd.kind = HB_KIND_SWIGLU;
@@ -1276,6 +1289,111 @@ int hb_engine_experts(hb_engine* e, uint32_t experts, uint32_t top_k, uint32_t h
         }
     }
     e->logf("[autotune] experts, %u rows -> tiles of %u rows", m, *bm_out);
+    hb_engine::ExpertsPick ep;
+    for (int i = 0; i < 4; i++) ep.kernels[i] = kernels[i];
+    ep.bm = *bm_out;
+    e->experts_pick[ekey] = ep;
+    return HB_OK;
+}
+
+// The picks as text, one line per choice, tab-separated: the choice's kind
+// and key, then for each kernel of it its name and its descriptor's fields
+// (decimal, in hb_desc order; "-" for none).  hb_engine_pin reads the same.
+static std::string desc_text(hb_gpu* g, int32_t k) {
+    if (k < 0) return "-\t-";
+    const hb_desc* d = kernel_desc(g, k);
+    std::string s = std::string(hb_kernel_name(g, k)) + "\t";
+    const uint32_t* w = (const uint32_t*)d;
+    for (size_t i = 0; i < sizeof(hb_desc) / 4; i++) s += (i ? " " : "") + std::to_string(w[i]);
+    return s;
+}
+
+int hb_engine_picks(hb_engine* e, char* buf, uint64_t cap, uint64_t* len) {
+    if (!e->g) return fail(HB_ERR_INVALID, "picks: an engine without a context");
+    std::string s;
+    for (const auto& kv : e->gemm_pick) s += "gemm\t" + kv.first + "\t" + desc_text(e->g, kv.second) + "\n";
+    for (const auto& kv : e->gate_up_pick)
+        s += "gate_up\t" + kv.first + "\t" + desc_text(e->g, kv.second.first) + "\t" +
+             desc_text(e->g, kv.second.second) + "\n";
+    for (const auto& kv : e->mv_pick) {
+        int32_t k;
+        int rc = e->build(kv.second, &k);
+        if (rc) return rc;
+        s += "mv\t" + kv.first + "\t" + desc_text(e->g, k) + "\n";
+    }
+    for (const auto& kv : e->experts_pick) {
+        s += "experts\t" + kv.first + "\t" + std::to_string(kv.second.bm);
+        for (int i = 0; i < 4; i++) s += "\t" + desc_text(e->g, kv.second.kernels[i]);
+        s += "\n";
+    }
+    *len = s.size();
+    if (buf && cap) {
+        const uint64_t n = std::min<uint64_t>(cap - 1, s.size());
+        memcpy(buf, s.data(), n);
+        buf[n] = 0;
+    }
+    return HB_OK;
+}
+
+int hb_engine_pin(hb_engine* e, const char* text) {
+    if (!e->g) return fail(HB_ERR_INVALID, "pin: an engine without a context");
+    std::istringstream in(text ? text : "");
+    std::string line;
+    int no = 0;
+    while (std::getline(in, line)) {
+        no++;
+        if (line.empty()) continue;
+        std::vector<std::string> f;
+        std::string cell;
+        std::istringstream ls(line);
+        while (std::getline(ls, cell, '\t')) f.push_back(cell);
+        auto bad = [&](const std::string& why) {
+            return fail(HB_ERR_INVALID, "pin, line " + std::to_string(no) + ": " + why);
+        };
+        // Builds the kernel of fields f[at] (name) and f[at + 1] (descriptor).
+        auto kernel_at = [&](size_t at, int32_t* k) -> int {
+            if (at + 1 >= f.size()) return bad("too few fields");
+            if (f[at] == "-") {
+                *k = -1;
+                return HB_OK;
+            }
+            hb_desc d{};
+            uint32_t* w = (uint32_t*)&d;
+            std::istringstream ds(f[at + 1]);
+            for (size_t i = 0; i < sizeof(hb_desc) / 4; i++)
+                if (!(ds >> w[i])) return bad("descriptor of " + f[at]);
+            int rc = e->build(d, k);
+            if (rc) return rc;
+            if (f[at] != hb_kernel_name(e->g, *k))
+                return bad("the descriptor builds " + std::string(hb_kernel_name(e->g, *k)) + ", not " + f[at]);
+            return HB_OK;
+        };
+        int rc;
+        if (f.size() < 2) return bad("no key");
+        if (f[0] == "gemm") {
+            int32_t k;
+            if ((rc = kernel_at(2, &k))) return rc;
+            e->gemm_pick[f[1]] = k;
+        } else if (f[0] == "gate_up") {
+            int32_t a, b;
+            if ((rc = kernel_at(2, &a)) || (rc = kernel_at(4, &b))) return rc;
+            e->gate_up_pick[f[1]] = {a, b};
+        } else if (f[0] == "mv") {
+            int32_t k;
+            if ((rc = kernel_at(2, &k))) return rc;
+            if (k < 0) return bad("no matvec kernel");
+            e->mv_pick[f[1]] = *kernel_desc(e->g, k);
+        } else if (f[0] == "experts") {
+            if (f.size() < 11) return bad("too few fields");
+            hb_engine::ExpertsPick ep;
+            ep.bm = (uint32_t)std::stoul(f[2]);
+            for (int i = 0; i < 4; i++)
+                if ((rc = kernel_at(3 + 2 * i, &ep.kernels[i]))) return rc;
+            e->experts_pick[f[1]] = ep;
+        } else {
+            return bad("unknown kind " + f[0]);
+        }
+    }
     return HB_OK;
 }
 

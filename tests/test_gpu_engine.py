@@ -303,3 +303,39 @@ def test_prefill_mlp_from_checkpoint_in_blocks(gpu, tmp_path):
         for b in states + [X]:
             gpu.free(b)
         mlp.free()
+
+
+def test_picks_pinned_in_another_engine(gpu):
+    """hb_engine_picks / hb_engine_pin: a second engine seeded with the
+    first one's choices returns the same kernels without timing them, and a
+    descriptor that does not build the recorded name is refused."""
+    m, k, n = 256, 512, 1024
+    x = hb.normal_bf16(31, 1.0, (m, k))
+    w = hb.normal_bf16(32, 0.02, (n, k))
+    st = gpu.alloc_with(np.array([0, 0, 0, m], np.uint32))
+    W, X, Y = gpu.alloc_with(w), gpu.alloc_with(x), gpu.alloc(m * n * 2)
+    xv, yv = gpu.alloc_with(hb.normal_bf16(33, 1.0, (4, k))), gpu.alloc(4 * n * 2)
+    try:
+        with hb.Engine(gpu, "") as a:
+            ka = a.gemm(k, n, 0, hb.r(st), hb.r(W), hb.r(X), hb.r(Y), m)
+            va = a.mv(k, n, 0, 4, [hb.r(W)], hb.r(xv), hb.r(yv))
+            text = a.picks()
+        lines = text.splitlines()
+        assert any(ln.startswith("gemm\t%dx%d Bf16, %d rows\t" % (k, n, m)) for ln in lines), text
+        assert any(ln.startswith("mv\t") for ln in lines), text
+        with hb.Engine(gpu, "") as b:
+            b.pin(text)
+            kb = b.gemm(k, n, 0, hb.r(st), hb.r(W), hb.r(X), hb.r(Y), m)
+            vb = b.mv(k, n, 0, 4, [hb.r(W)], hb.r(xv), hb.r(yv))
+            assert "[autotune]" not in b.log()  # nothing timed
+            assert gpu.kernel_name(kb) == gpu.kernel_name(ka)
+            assert gpu.kernel_name(vb) == gpu.kernel_name(va)
+            gl = [ln for ln in lines if ln.startswith("gemm\t")][0].split("\t")
+            gl[2] = "gemm_mma_not_this_name"
+            with pytest.raises(hb.HerbertError, match="not gemm_mma_not_this_name"):
+                b.pin("\t".join(gl))
+            with pytest.raises(hb.HerbertError, match="unknown kind"):
+                b.pin("conv\tkey\tname\t1 2 3")
+    finally:
+        for buf in (st, W, X, Y, xv, yv):
+            gpu.free(buf)
