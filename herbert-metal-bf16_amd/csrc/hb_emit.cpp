@@ -421,8 +421,6 @@ uint32_t groups_of(const hb_desc& d, uint32_t m) {
             return m;  // a workgroup per row
         case HB_KIND_ROUND_PROBE:
             return (1u << 24) / 256;  // one pattern per thread
-        case HB_KIND_MV_CHAIN:
-            return d.persist;  // one persistent workgroup per CU
         default:
             return 0;
     }
@@ -516,14 +514,6 @@ int check_bindings(const hb_desc& d, const uint64_t* s, uint32_t nbind, uint32_t
             if ((rc = need(s, 0, 16, "state"))) return rc;
             if ((rc = need(s, 1, (uint64_t)d.ksplit * mm * d.n * 4, "slabs"))) return rc;
             return need(s, 2, mm * d.n * out_bytes(d.out), "Y");
-        case HB_KIND_MV_CHAIN:
-            // d.n phases: the table's three device addresses each, the sync
-            // words (a counter per phase, then the error word).
-            if (m < 1 || m > d.mv_m)
-                return fail(HB_ERR_INVALID, "mv_chain of " + std::to_string(m) + " rows: 1.." +
-                                                std::to_string(d.mv_m));
-            if ((rc = need(s, 0, (uint64_t)d.n * 24, "table"))) return rc;
-            return need(s, 1, ((uint64_t)d.n + 1) * 4, "sync");
         case HB_KIND_COMBINE:
             if ((rc = need(s, 0, mm * d.top_k * d.n * 2, "y"))) return rc;
             if ((rc = need(s, 1, mm * k2 * 4, "route"))) return rc;

@@ -59,8 +59,6 @@ struct Kernel {
     // A split-K GEMM (desc.ksplit > 1): the kernel that adds its parts'
     // slabs and applies Out, launched after it by every launch of this one.
     int32_t reduce = -1;
-    // A decode chain (HB_KIND_MV_CHAIN): its phases' (K, N, out) triples.
-    std::vector<uint32_t> chain;
 };
 
 // The descriptor kind of a split-K GEMM's second kernel (built by the
@@ -73,7 +71,6 @@ uint64_t workspace_of(const hb_desc& d, uint32_t m);
 
 struct hb_gpu {
     int device = 0;
-    int cus = 0;  // compute units
     hipStream_t stream = nullptr;
     hipEvent_t ev0 = nullptr, ev1 = nullptr;
     std::vector<hb::Buffer> bufs;

@@ -193,19 +193,11 @@ static int compile(const Emitted& em, const std::string& arch, std::string* code
     return HB_OK;
 }
 
-static int load_emitted(hb_gpu* g, Kernel* k);
-
 static int load_kernel(hb_gpu* g, const hb_desc& d, Kernel* k) {
     k->desc = d;
     int rc = emit(d, &k->em);
     if (rc) return rc;
     manifest_add(d);
-    return load_emitted(g, k);
-}
-
-// Compiles (or finds in the disk cache) and loads k->em.
-static int load_emitted(hb_gpu* g, Kernel* k) {
-    int rc;
     auto t0 = std::chrono::steady_clock::now();
     std::string code;
     rc = compile(k->em, g->arch, &code);
@@ -243,12 +235,6 @@ static int launch_one(hb_gpu* g, const Kernel& k, void** ptrs, uint32_t nptr, ui
     void* args[12];
     for (uint32_t i = 0; i < nptr; i++) args[i] = &ptrs[i];
     args[nptr] = &m;
-    if (k.desc.kind == HB_KIND_MV_CHAIN) {
-        // Its workgroups wait for each other: every one must be resident,
-        // which a cooperative launch guarantees (or refuses).
-        HB_HIP(hipModuleLaunchCooperativeKernel(k.fn, groups, 1, 1, k.em.threads, 1, 1, 0, g->stream, args));
-        return HB_OK;
-    }
     HB_HIP(hipModuleLaunchKernel(k.fn, groups, 1, 1, k.em.threads, 1, 1, 0, g->stream, args,
                                  nullptr));
     return HB_OK;
@@ -337,7 +323,6 @@ int hb_open(int device, hb_gpu** out) {
              p.multiProcessorCount, p.totalGlobalMem / 1073741824.0, p.gcnArchName,
              (size_t)p.sharedMemPerBlock / 1024);
     g->summary = buf;
-    g->cus = p.multiProcessorCount;
     if ((e = hipStreamCreateWithFlags(&g->stream, hipStreamNonBlocking)) != hipSuccess ||
         (e = hipEventCreate(&g->ev0)) != hipSuccess || (e = hipEventCreate(&g->ev1)) != hipSuccess) {
         delete g;
@@ -509,90 +494,6 @@ int hb_kernel_build(hb_gpu* g, const hb_desc* desc, int32_t* kernel) {
     g->kernels.push_back(k);
     *kernel = (int32_t)(g->kernels.size() - 1);
     g->by_name[em.name] = *kernel;
-    return HB_OK;
-}
-
-int hb_mv_chain_build(hb_gpu* g, const uint32_t* shapes, uint32_t nph, uint32_t mv_m, uint32_t groups,
-                      int32_t* kernel) {
-    if (!nph || nph > 64 || mv_m < 1 || mv_m > 8)
-        return fail(HB_ERR_INVALID, "mv_chain: 1..64 phases of 1..8 rows");
-    uint32_t kmax = 0;
-    std::string ks, ns, os, key;
-    for (uint32_t p = 0; p < nph; p++) {
-        const uint32_t k = shapes[3 * p], n = shapes[3 * p + 1], out = shapes[3 * p + 2];
-        if (!k || k % 512 || !n || out > HB_OUT_RESIDUAL)
-            return fail(HB_ERR_UNSUPPORTED, "mv_chain phase " + std::to_string(p) +
-                                                ": K a multiple of 512, N > 0, Out Bf16 / F32 / Residual");
-        kmax = k > kmax ? k : kmax;
-        ks += (p ? "," : "") + std::to_string(k);
-        ns += (p ? "," : "") + std::to_string(n);
-        os += (p ? "," : "") + std::to_string(out);
-    }
-    if ((uint64_t)mv_m * kmax * 2 > 160 * 1024 - 256)
-        return fail(HB_ERR_UNSUPPORTED, "mv_chain: m * K * 2 bytes of x exceed the LDS");
-    if (!groups) groups = (uint32_t)g->cus;
-    Kernel k;
-    k.desc = hb_desc{};
-    k.desc.kind = HB_KIND_MV_CHAIN;
-    k.desc.n = nph;
-    k.desc.k = kmax;
-    k.desc.mv_m = mv_m;
-    k.desc.persist = groups;
-    k.chain.assign(shapes, shapes + 3 * nph);
-    key = ks + "/" + ns + "/" + os;
-    char name[96];
-    snprintf(name, sizeof name, "mv_chain_p%u_m%u_g%u_%08llx", nph, mv_m, groups,
-             (unsigned long long)(fnv1a(key) & 0xffffffffull));
-    auto it = g->by_name.find(name);
-    if (it != g->by_name.end()) {
-        *kernel = it->second;
-        return HB_OK;
-    }
-    k.em.name = name;
-    k.em.source = "mv_chain.hip";
-    k.em.threads = 512;
-    k.em.nbind = 2;
-    k.em.defines = {"-DHB_MV_M=" + std::to_string(mv_m), "-DHB_NPH=" + std::to_string(nph),
-                    "-DHB_PH_K=" + ks, "-DHB_PH_N=" + ns, "-DHB_PH_OUT=" + os,
-                    "-DHB_CPL=" + std::to_string(kmax / 512), "-DHB_WAVES=8"};
-    int rc = load_emitted(g, &k);
-    if (rc) return rc;
-    g->kernels.push_back(k);
-    *kernel = (int32_t)(g->kernels.size() - 1);
-    g->by_name[name] = *kernel;
-    return HB_OK;
-}
-
-int hb_mv_chain_table(hb_gpu* g, int32_t kernel, const hb_range* io, uint32_t m, hb_range table) {
-    if (kernel < 0 || (size_t)kernel >= g->kernels.size() || g->kernels[kernel].desc.kind != HB_KIND_MV_CHAIN)
-        return fail(HB_ERR_INVALID, "mv_chain_table: not a chain kernel");
-    const Kernel& k = g->kernels[kernel];
-    const uint32_t nph = k.desc.n;
-    if (m < 1 || m > k.desc.mv_m) return fail(HB_ERR_INVALID, "mv_chain_table: m out of range");
-    std::vector<uint64_t> words(3 * nph);
-    for (uint32_t p = 0; p < nph; p++) {
-        const uint64_t kk = k.chain[3 * p], n = k.chain[3 * p + 1], out = k.chain[3 * p + 2];
-        const uint64_t need[3] = {n * kk * 2, m * kk * 2, m * n * (out == HB_OUT_F32 ? 4 : 2)};
-        const char* what[3] = {"W", "x", "y"};
-        for (int i = 0; i < 3; i++) {
-            char* ptr;
-            uint64_t size;
-            int rc = resolve(g, io[3 * p + i], &ptr, &size);
-            if (rc) return rc;
-            if (size < need[i])
-                return fail(HB_ERR_INVALID, "mv_chain phase " + std::to_string(p) + ": " + what[i] + " holds " +
-                                                std::to_string(size) + " bytes, needs " + std::to_string(need[i]));
-            words[3 * p + i] = (uint64_t)(uintptr_t)ptr;
-        }
-    }
-    char* tp;
-    uint64_t tsize;
-    int rc = resolve(g, table, &tp, &tsize);
-    if (rc) return rc;
-    if (tsize < words.size() * 8) return fail(HB_ERR_INVALID, "mv_chain_table: the table range is too small");
-    HB_HIP(hipSetDevice(g->device));
-    HB_HIP(hipStreamSynchronize(g->stream));
-    HB_HIP(hipMemcpy(tp, words.data(), words.size() * 8, hipMemcpyHostToDevice));
     return HB_OK;
 }
 

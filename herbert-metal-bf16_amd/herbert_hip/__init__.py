@@ -89,7 +89,6 @@ class Kind(enum.IntEnum):
     ROUND_PROBE = 11
     MOE_OUT = 12
     RMSNORM = 13
-    MV_CHAIN = 14
 
 
 class Rows(enum.IntEnum):
@@ -398,18 +397,6 @@ class Gpu:
         check(lib.hb_time(self.h, arr, len(ops), int(reps), ctypes.byref(s)))
         return s.value
 
-    def mv_chain(self, shapes, mv_m, groups=0):
-        """hb_mv_chain_build: shapes [(K, N, out)] of the phases -> kernel."""
-        flat = (_u32 * (3 * len(shapes)))(*[int(v) for sh in shapes for v in sh])
-        k = _i32()
-        check(lib.hb_mv_chain_build(self.h, flat, len(shapes), int(mv_m), int(groups), ctypes.byref(k)))
-        return k.value
-
-    def mv_chain_table(self, kernel, io, m, table):
-        """hb_mv_chain_table: io [(W, x, y) Ranges] per phase into `table`."""
-        arr = (Range * (3 * len(io)))(*[rr for ph in io for rr in ph])
-        check(lib.hb_mv_chain_table(self.h, int(kernel), arr, int(m), table))
-
     def graph(self, ops):
         """The ops recorded into a HIP graph (hb_graph_record): a Graph."""
         arr = (Op * len(ops))(*ops)
@@ -452,8 +439,6 @@ def tune_check(tune):
 
 lib.hb_engine_picks.argtypes = [_P, ctypes.c_char_p, _u64, ctypes.POINTER(_u64)]
 lib.hb_engine_pin.argtypes = [_P, ctypes.c_char_p]
-lib.hb_mv_chain_build.argtypes = [_P, ctypes.POINTER(_u32), _u32, _u32, _u32, ctypes.POINTER(_i32)]
-lib.hb_mv_chain_table.argtypes = [_P, _i32, ctypes.POINTER(Range), _u32, Range]
 lib.hb_graph_record.argtypes = [_P, ctypes.POINTER(Op), _u32, ctypes.POINTER(_P)]
 lib.hb_graph_launch.argtypes = [_P, _u32]
 lib.hb_graph_time.argtypes = [_P, _u32, ctypes.POINTER(ctypes.c_double)]

@@ -83,8 +83,7 @@ enum hb_kind {
     HB_KIND_COMBINE = 10,    /* moe_combine (qwen_kernels.rs:2119-2165) */
     HB_KIND_ROUND_PROBE = 11, /* herbert-metal-probe round (bin/herbert-metal-probe.rs:7-11) */
     HB_KIND_MOE_OUT = 12,    /* moe_out (qwen_kernels.rs:2163-2214): the MoE block's end */
-    HB_KIND_RMSNORM = 13,    /* rmsnorm (kernels.rs:48-103): the block's input norm, rows of n */
-    HB_KIND_MV_CHAIN = 14    /* a decode step's matvecs in one launch (hb_mv_chain_build) */
+    HB_KIND_RMSNORM = 13     /* rmsnorm (kernels.rs:48-103): the block's input norm, rows of n */
 };
 
 enum hb_out { /* Out (kernels.rs:30-43) */
@@ -251,25 +250,6 @@ int hb_time(hb_gpu *gpu, const hb_op *ops, uint32_t nops, uint32_t reps, double 
  * *seconds the whole run. */
 int hb_time_each(hb_gpu *gpu, const hb_op *ops, uint32_t nops, uint32_t reps, double *seconds,
                  double *op_seconds);
-
-/* A decode step's matvecs in one launch (no counterpart kernel in the
- * reference, which records the step's matvec dispatches into one command
- * buffer, QwenEngine::step, qwen.rs:3177): `nph` phases, shapes[3p..3p+2] =
- * (K, N, out) of phase p (K a multiple of 512; Out Bf16, F32 or Residual),
- * y_p = x_p . W_p^T over up to mv_m (<= 8) rows with f32 sums, each phase
- * started only after every output of the one before it is written (the
- * order consecutive launches give).  One cooperative launch of `groups`
- * persistent workgroups (0: one per CU).  Bindings of its launch: the
- * phase table (hb_mv_chain_table), the sync words (nph + 1 u32, zero
- * before the first launch; the launch leaves them zero, except the last,
- * the error word, set when a wait gave up).  m*K_max*2 bytes of x must fit
- * the LDS. */
-int hb_mv_chain_build(hb_gpu *gpu, const uint32_t *shapes, uint32_t nph, uint32_t mv_m, uint32_t groups,
-                      int32_t *kernel);
-/* Writes the chain's phase table into `table` (24 bytes a phase): io holds
- * the W, x, y ranges of each phase in turn (3 * nph), checked against the
- * phase's shape and m rows.  Synchronizes the context's stream first. */
-int hb_mv_chain_table(hb_gpu *gpu, int32_t kernel, const hb_range *io, uint32_t m, hb_range table);
 
 /* A recorded op sequence: the reference encodes a decode step's ops into one
  * command buffer and submits it (QwenEngine::step, qwen.rs:3177); here the
