@@ -488,6 +488,21 @@ def counter_run(g, hb):
 # busy cycles per SIMD (1024 SIMDs), as microseconds at 2.4 GHz, to set
 # beside the kernel's own duration.
 SIMDS, CLOCK_MHZ = 1024, 2400.0
+# How profiles/counters.json and counters_summary.txt are made (P = picks
+# file, from a plain run; the three counter passes run on those picks, so
+# every pass measures the same kernels).
+COUNTER_COMMANDS = [
+    "commands (cd /tmp && export TMPDIR=/tmp first; R = the repository):",
+    "  python3 R/bench.py --no-cpu --picks-out P",
+    "  rocprofv3 --pmc FETCH_SIZE -d C1 -o run --output-format csv -- "
+    "python3 R/bench.py --counter-run --picks-in P --steps 3 --warmup 1 --no-cpu > B",
+    "  rocprofv3 --pmc WRITE_SIZE TCC_HIT_sum TCC_MISS_sum -d C2 -o run --output-format csv -- "
+    "python3 R/bench.py --counter-run --picks-in P --steps 3 --warmup 1 --no-cpu",
+    "  rocprofv3 --pmc SQ_INSTS_MFMA SQ_VALU_MFMA_BUSY_CYCLES SQ_BUSY_CYCLES SQ_WAIT_INST_ANY SQ_WAVE_CYCLES "
+    "-d C3 -o run --output-format csv -- python3 R/bench.py --counter-run --picks-in P --steps 3 --warmup 1 --no-cpu",
+    "  python3 R/bench.py --counter-summary B C1/run_counter_collection.csv C2/run_counter_collection.csv "
+    "C3/run_counter_collection.csv",
+    ""]
 
 
 def counter_summary(bench_out, csvs):
@@ -550,9 +565,10 @@ def counter_summary(bench_out, csvs):
     path = os.path.join(ROOT, "profiles", "counters.json")
     with open(path, "w") as fh:
         json.dump(out, fh, indent=1, sort_keys=True)
-    lines = ["per region and kernel, medians over its full-size dispatches (bytes scaled by the calibration "
-             "copy: fetch x%.4f, write x%.4f); mfma_us = SQ_VALU_MFMA_BUSY_CYCLES / %d SIMDs / %.0f MHz"
-             % (sf, sw, SIMDS, CLOCK_MHZ), ""]
+    lines = COUNTER_COMMANDS + [
+        "per region and kernel, medians over its full-size dispatches (bytes scaled by the calibration "
+        "copy: fetch x%.4f, write x%.4f); mfma_us = SQ_VALU_MFMA_BUSY_CYCLES / %d SIMDs / %.0f MHz"
+        % (sf, sw, SIMDS, CLOCK_MHZ), ""]
     for nm in names:
         if nm == "calibration" or nm not in out:
             continue
