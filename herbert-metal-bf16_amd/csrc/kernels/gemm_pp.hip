@@ -427,12 +427,11 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
             }
         };
         for_each([&](acc_t& v, u32 q, u64 at) HB_INLINE {
-            u32* d = (u32*)(slabs + part * slab + at);
-#pragma unroll
-            for (u32 e = 0; e < 4; e++) {
-                const float f = v[4 * q + e];
-                __hip_atomic_store(d + e, __float_as_uint(f), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
+            u64* d = (u64*)(slabs + part * slab + at);
+            __hip_atomic_store(d, (u64)__builtin_bit_cast(u32, v[4 * q]) | ((u64)__builtin_bit_cast(u32, v[4 * q + 1]) << 32),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(d + 1, (u64)__builtin_bit_cast(u32, v[4 * q + 2]) | ((u64)__builtin_bit_cast(u32, v[4 * q + 3]) << 32),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         });
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __shared__ u32 kf_last;
@@ -445,18 +444,23 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
         __syncthreads();
         if (!kf_last) return;
         for_each([&](acc_t& v, u32 q, u64 at) HB_INLINE {
+            float r[KSP][4];
+#pragma unroll
+            for (u32 p = 0; p < KSP; p++) {
+                if (p == part) continue;
+                const u64* d = (const u64*)(slabs + p * slab + at);
+                const u64 a = __hip_atomic_load(d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const u64 b = __hip_atomic_load(d + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                r[p][0] = __builtin_bit_cast(float, (u32)a);
+                r[p][1] = __builtin_bit_cast(float, (u32)(a >> 32));
+                r[p][2] = __builtin_bit_cast(float, (u32)b);
+                r[p][3] = __builtin_bit_cast(float, (u32)(b >> 32));
+            }
 #pragma unroll
             for (u32 e = 0; e < 4; e++) {
-                const float mine = v[4 * q + e];
-                float t = 0.0f;
+                float t = part == 0 ? v[4 * q + e] : r[0][e];
 #pragma unroll
-                for (u32 p = 0; p < KSP; p++) {
-                    const u32* d = (const u32*)(slabs + p * slab + at) + e;
-                    const float o = p == part ? mine
-                                              : __uint_as_float(__hip_atomic_load(d, __ATOMIC_RELAXED,
-                                                                                  __HIP_MEMORY_SCOPE_AGENT));
-                    t = p == 0 ? o : t + o;
-                }
+                for (u32 p = 1; p < KSP; p++) t = t + (p == part ? v[4 * q + e] : r[p][e]);
                 v[4 * q + e] = t;
             }
         });
