@@ -39,7 +39,6 @@ static bool is_gemm(uint32_t kind) {
 hb_desc with_defaults(const hb_desc& in) {
     hb_desc d = in;
     if (d.ksplit == 1) d.ksplit = 0;  // one part: no split
-    if (d.ksplit < 2) d.kfuse = 0;
     if (d.kind == HB_KIND_GEMM || d.kind == HB_KIND_GEMM_SWIGLU) {
         bool experts = d.rows_of != HB_ROWS_DENSE;
         if (!d.bm) d.bm = experts ? 32 : 128;
@@ -142,11 +141,9 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
                 return fail(HB_ERR_UNSUPPORTED,
                             "gemm split K: 2..16 parts, dense rows, K a multiple of bk x parts "
                             "(sched 3: an even count of K tiles per part)");
-            if (d.kfuse > 1 || (d.kfuse && (d.sched != 1 && d.sched != 2)))
-                return fail(HB_ERR_UNSUPPORTED, "gemm split K in one launch (kfuse): the pipelined schedules 1, 2");
             std::string band = d.band ? "_b" + std::to_string(d.band) : "";
             if (d.w_nt) band += "_wnt";
-            if (d.ksplit > 1) band += (d.kfuse ? "_ksf" : "_ks") + std::to_string(d.ksplit);
+            if (d.ksplit > 1) band += "_ks" + std::to_string(d.ksplit);
             if (d.sched) band += d.sched == 1 ? "_pp" : d.sched == 2 ? "_pp2" : "_il";
             snprintf(name, sizeof name, "gemm_mma%s_%ux%u_%s%s_t%ux%u_k%u_w%ux%u_x%u_d%u%s_s%u_o%u%s%s",
                      swi ? "_swiglu" : "", d.k, d.n, out_tag(d.out), d.m_first ? "_mf" : "", d.bn,
@@ -166,10 +163,9 @@ static int emit_kind(const hb_desc& d, Emitted* e) {
                           D("HB_BAND", d.band), D("HB_W_NT", d.w_nt)};
             if (d.ksplit > 1) {
                 // The parts' f32 sums into the workspace; Out is the second
-                // kernel's, or (kfuse) the last part's.
-                if (!d.kfuse) e->defines[2] = D("HB_OUT", HB_OUT_F32);
+                // kernel's.
+                e->defines[2] = D("HB_OUT", HB_OUT_F32);
                 e->defines.push_back(D("HB_KSPLIT", d.ksplit));
-                e->defines.push_back(D("HB_KFUSE", d.kfuse));
             }
             if (d.sched) {
                 e->defines.push_back(D("HB_SCHED", d.sched == 3 ? 3 : 1));
@@ -432,7 +428,7 @@ uint32_t groups_of(const hb_desc& d, uint32_t m) {
 
 uint64_t workspace_of(const hb_desc& d, uint32_t m) {
     if (d.kind != HB_KIND_GEMM || d.ksplit < 2) return 0;
-    return WS_SLABS + (uint64_t)d.ksplit * m * d.n * 4;
+    return (uint64_t)d.ksplit * m * d.n * 4;
 }
 
 static int need(const uint64_t* sizes, uint32_t i, uint64_t bytes, const char* what) {
@@ -456,10 +452,6 @@ int check_bindings(const hb_desc& d, const uint64_t* s, uint32_t nbind, uint32_t
             if ((rc = need(s, 1, nw * k * 2, "W"))) return rc;
             if ((rc = need(s, 2, mm * k * 2, "X"))) return rc;
             if ((rc = need(s, 3, mm * yn * out_bytes(d.out), "Y"))) return rc;
-            if (d.kind == HB_KIND_GEMM && d.kfuse && d.ksplit > 1 &&
-                (uint64_t)cdiv(m, d.bm) * cdiv(d.n, d.bn) > WS_COUNTERS)
-                return fail(HB_ERR_INVALID, "gemm split K in one launch: more than " +
-                                                std::to_string(WS_COUNTERS) + " tiles a part");
         } else {
             uint64_t pairs = mm * d.top_k;
             if ((rc = need(s, 1, (uint64_t)d.experts * nw * k * 2, "W"))) return rc;

@@ -65,11 +65,6 @@ struct Kernel {
 // library with its GEMM, never named by a caller).
 constexpr uint32_t KIND_SPLITK_REDUCE = 0xfffe;
 // Workspace bytes a launch of `d` over m rows needs (split-K slabs), 0 if none.
-// The workspace: WS_SLABS bytes of tile counters (one u32 per tile of a
-// one-launch split, zero between launches: zeroed when the workspace is
-// allocated, and every launch's last parts set theirs back), then the slabs.
-constexpr uint64_t WS_SLABS = 64 * 1024;
-constexpr uint32_t WS_COUNTERS = WS_SLABS / 4;
 uint64_t workspace_of(const hb_desc& d, uint32_t m);
 
 }  // namespace hb

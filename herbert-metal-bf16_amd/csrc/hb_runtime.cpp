@@ -225,7 +225,6 @@ static int ensure_ws(hb_gpu* g, uint64_t bytes) {
     const uint64_t sz = (bytes + (1ull << 20) - 1) & ~((1ull << 20) - 1);
     HB_HIP(hipMalloc(&g->ws, sz));
     g->ws_bytes = sz;
-    HB_HIP(hipMemset(g->ws, 0, WS_SLABS));  // the one-launch split's tile counters
     return HB_OK;
 }
 
@@ -245,22 +244,14 @@ static int launch_one(hb_gpu* g, const Kernel& k, void** ptrs, uint32_t nptr, ui
 // (ensure_ws has sized it), then its reduce from there into Y.
 static int launch_raw(hb_gpu* g, const Kernel& k, void** ptrs, uint32_t nptr, uint32_t m,
                       uint32_t groups) {
-    const bool fused = k.desc.kind == HB_KIND_GEMM && k.desc.ksplit > 1 && k.desc.kfuse;
-    if (k.reduce < 0 && !fused) return launch_one(g, k, ptrs, nptr, m, groups);
+    if (k.reduce < 0) return launch_one(g, k, ptrs, nptr, m, groups);
     void* p[10];
     for (uint32_t i = 0; i < nptr; i++) p[i] = ptrs[i];
-    if (fused) {
-        // One launch: Y stays; the workspace (counters, then slabs) rides in
-        // the list binding, which dense rows do not use.
-        p[4] = g->ws;
-        return launch_one(g, k, p, nptr, m, groups);
-    }
-    void* slabs = (char*)g->ws + WS_SLABS;
-    p[3] = slabs;
+    p[3] = g->ws;
     int rc = launch_one(g, k, p, nptr, m, groups);
     if (rc) return rc;
     const Kernel& r = g->kernels[k.reduce];
-    void* q[3] = {ptrs[0], slabs, ptrs[3]};
+    void* q[3] = {ptrs[0], g->ws, ptrs[3]};
     return launch_one(g, r, q, 3, m, groups_of(r.desc, m));
 }
 
@@ -488,7 +479,7 @@ int hb_kernel_build(hb_gpu* g, const hb_desc* desc, int32_t* kernel) {
     Kernel k;
     rc = load_kernel(g, d, &k);
     if (rc) return rc;
-    if (d.kind == HB_KIND_GEMM && d.ksplit > 1 && !d.kfuse) {
+    if (d.kind == HB_KIND_GEMM && d.ksplit > 1) {
         // Its second kernel, built (or found) first.
         hb_desc rd{};
         rd.kind = KIND_SPLITK_REDUCE;

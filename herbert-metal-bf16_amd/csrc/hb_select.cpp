@@ -232,7 +232,7 @@ struct Tune {
 // indexes this table (gemm.mma=1).
 struct Form {
     const char* name;
-    uint32_t bm, bn, bk, wm, wn, mfma, dbuf, dma, order, band, sched, ksplit, kfuse;
+    uint32_t bm, bn, bk, wm, wn, mfma, dbuf, dma, order, band, sched, ksplit;
 };
 const Form kForms[10] = {
     {"mma", 128, 128, 64, 2, 2, 16, 1, 1, 1},
@@ -318,18 +318,6 @@ const Form kSplitForms[] = {
     {"pp_t128x256_ks4", 128, 256, 32, 2, 4, 16, 3, 1, 1, 0, 1, 4},
     {"pp_t256x256_ks2", 256, 256, 32, 4, 2, 16, 3, 1, 1, 0, 1, 2},
     {"pp_t256x256_ks4", 256, 256, 32, 4, 2, 16, 3, 1, 1, 0, 1, 4},
-    // The same ping-pong splits in one launch (hb_desc.kfuse): the tile's
-    // last part adds the slabs, no second kernel (which, with the launch gap
-    // it adds, cost 7-10 us of a 25-35 us split GEMM at M = 512).
-    {"pp_t256x160_k64_ks2f", 256, 160, 64, 4, 2, 16, 2, 1, 1, 0, 1, 2, 1},
-    {"pp_t256x160_k64_ks4f", 256, 160, 64, 4, 2, 16, 2, 1, 1, 0, 1, 4, 1},
-    {"pp_t128x160_k64_ks2f", 128, 160, 64, 4, 2, 16, 3, 1, 1, 0, 1, 2, 1},
-    {"pp_t128x160_k64_ks4f", 128, 160, 64, 4, 2, 16, 3, 1, 1, 0, 1, 4, 1},
-    {"pp_t128x256_ks2f", 128, 256, 32, 2, 4, 16, 3, 1, 1, 0, 1, 2, 1},
-    {"pp_t128x256_ks4f", 128, 256, 32, 2, 4, 16, 3, 1, 1, 0, 1, 4, 1},
-    {"pp_t256x256_ks2f", 256, 256, 32, 4, 2, 16, 3, 1, 1, 0, 1, 2, 1},
-    {"pp_t256x256_ks4f", 256, 256, 32, 4, 2, 16, 3, 1, 1, 0, 1, 4, 1},
-    {"pp_t128x160_k64_ks8f", 128, 160, 64, 4, 2, 16, 3, 1, 1, 0, 1, 8, 1},
 };
 // The fused [gate | up] + SwiGLU forms (gate_up_pipes, qwen.rs:2148-2193):
 // bn W rows per tile = bn/2 features.
@@ -360,7 +348,6 @@ hb_desc form_desc(const Form& f, uint32_t k, uint32_t n, uint32_t out, bool mf) 
     d.band = f.band;
     d.sched = f.sched;
     d.ksplit = f.ksplit;
-    d.kfuse = f.kfuse;
     return d;
 }
 

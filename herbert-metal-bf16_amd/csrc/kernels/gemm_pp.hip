@@ -66,8 +66,7 @@
 // HB_GRP (ping-pong: which waves form a group: 0 waves 0-3 / 4-7, 1 even /
 // odd waves), HB_KSPLIT (s > 1: K cut into s parts, part p's f32 sums into
 // slab p of Y, [m_launch][N] floats each, as in gemm_mfma.hip; a second
-// kernel adds the slabs), HB_KFUSE (with HB_KSPLIT: one launch, the tile's
-// last part adds the slabs and applies Out; the workspace in `list`).
+// kernel adds the slabs).
 //
 // Bindings: state (u32[4], state[3] = rows), W, X, Y, list, tiles (unused:
 // dense rows); then the rows the launch was sized for (m_launch).
@@ -111,13 +110,7 @@ constexpr u32 LMIN = NXL / NWV + NWL / NWV;  // loads per stage of every wave
 static_assert(HB_SCHED == 1 || HB_SCHED == 3, "schedule 1 or 3");
 static_assert(WM * WN == NWV, "eight wavefronts (ping-pong) or four");
 static_assert(K % (BK * KSP) == 0, "K a multiple of the K step times the parts");
-#ifndef HB_KFUSE
-#define HB_KFUSE 0
-#endif
-static_assert(KSP == 1 || OUT == 1 || HB_KFUSE, "split K: f32 partial sums (or the last part's Out)");
-static_assert(!HB_KFUSE || KSP > 1, "one-launch split: 2 parts or more");
-// The one-launch split's workspace: 64 KiB of tile counters, then the slabs.
-constexpr u64 KF_SLABS = 64 * 1024;
+static_assert(KSP == 1 || OUT == 1, "split K: f32 partial sums");
 static_assert(N % 4 == 0, "N a multiple of 4");
 static_assert(TM % FM == 0 && TN % FM == 0, "wave tile a multiple of the MFMA block");
 static_assert(BK % KS == 0 && (CH & (CH - 1)) == 0, "K step");
@@ -401,73 +394,7 @@ extern "C" __global__ __launch_bounds__(NT) void HB_NAME(
     step(KT - 1, st, 1, bconst<false>{});
     }
 
-#if HB_KFUSE
-    // Split K in one launch: this part's f32 sums to its slab, then a count
-    // per tile; the tile's last part adds the slabs in part order (its own
-    // sums from registers at its place: the bits of the two-kernel form) and
-    // writes Y as Out says.  The workspace (the list binding): the tile
-    // counters, then the slabs.  Slab stores and loads are agent-scope (no
-    // stale line in another XCD's L2 answers them); the count is an
-    // agent-scope atomic after this part's stores are complete.
-    {
-        u32* const cnt = (u32*)list;
-        float* const slabs = (float*)((char*)list + KF_SLABS);
-        const u64 slab = (u64)m_launch * N;
-        auto for_each = [&](auto&& f) HB_INLINE {
-#pragma unroll
-            for (u32 j = 0; j < IM; j++) {
-                const u32 ml = wm * TM + j * FM + fr;
-#pragma unroll
-                for (u32 i = 0; i < IN; i++)
-#pragma unroll
-                    for (u32 q = 0; q < FM * FM / 256; q++) {
-                        const u32 n = n0 + wn * TN + i * FM + q * 8 + 4 * fc;
-                        if (ml < rows && n < N) f(acc[i][j], q, (u64)(row0 + ml) * N + n);
-                    }
-            }
-        };
-        for_each([&](acc_t& v, u32 q, u64 at) HB_INLINE {
-            u64* d = (u64*)(slabs + part * slab + at);
-            __hip_atomic_store(d, (u64)__builtin_bit_cast(u32, v[4 * q]) | ((u64)__builtin_bit_cast(u32, v[4 * q + 1]) << 32),
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(d + 1, (u64)__builtin_bit_cast(u32, v[4 * q + 2]) | ((u64)__builtin_bit_cast(u32, v[4 * q + 3]) << 32),
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        });
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        __shared__ u32 kf_last;
-        __syncthreads();
-        if (tid == 0) {
-            const u32 before = __hip_atomic_fetch_add(&cnt[g], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            kf_last = before == KSP - 1;
-            if (before == KSP - 1) __hip_atomic_store(&cnt[g], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-        __syncthreads();
-        if (!kf_last) return;
-        for_each([&](acc_t& v, u32 q, u64 at) HB_INLINE {
-            float r[KSP][4];
-#pragma unroll
-            for (u32 p = 0; p < KSP; p++) {
-                if (p == part) continue;
-                const u64* d = (const u64*)(slabs + p * slab + at);
-                const u64 a = __hip_atomic_load(d, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const u64 b = __hip_atomic_load(d + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                r[p][0] = __builtin_bit_cast(float, (u32)a);
-                r[p][1] = __builtin_bit_cast(float, (u32)(a >> 32));
-                r[p][2] = __builtin_bit_cast(float, (u32)b);
-                r[p][3] = __builtin_bit_cast(float, (u32)(b >> 32));
-            }
-#pragma unroll
-            for (u32 e = 0; e < 4; e++) {
-                float t = part == 0 ? v[4 * q + e] : r[0][e];
-#pragma unroll
-                for (u32 p = 1; p < KSP; p++) t = t + (p == part ? v[4 * q + e] : r[p][e]);
-                v[4 * q + e] = t;
-            }
-        });
-    }
-#else
     if constexpr (KSP > 1) Yv = (float*)Yv + (u64)part * m_launch * N;  // this part's slab
-#endif
     if constexpr (EPI_LDS) {
         epilogue_lds(lds, acc, tid, wm, wn, fr, fc, row0, rows, n0, Yv);
         return;

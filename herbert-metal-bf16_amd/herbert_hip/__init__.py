@@ -111,7 +111,7 @@ class Range(ctypes.Structure):
 _DESC_FIELDS = ["kind", "k", "n", "out", "rows_of", "m_first", "bm", "bn", "bk", "wm", "wn",
                 "mfma", "dbuf", "swz", "order", "mv_m", "split", "persist", "rows", "form",
                 "top_k", "experts", "tiles", "rows_max", "lds_dma", "unroll", "band", "xsrc", "eps_bits", "plus_one",
-                "x_lds", "w_nt", "mv_waves", "sched", "ksplit", "kfuse"]
+                "x_lds", "w_nt", "mv_waves", "sched", "ksplit"]
 
 
 class Desc(ctypes.Structure):

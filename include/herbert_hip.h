@@ -188,12 +188,6 @@ typedef struct hb_desc {
      * allowed under stream capture), so launch a split kernel once at its
      * largest rows before capturing it. */
     uint32_t ksplit;
-    /* Split K (ksplit > 1) with the pipelined schedules (sched 1, 2), 1: one
-     * launch -- each part writes its f32 sums to the workspace and counts
-     * itself in (an agent-scope atomic per tile); the tile's last part to
-     * finish adds the parts in order 0..ksplit-1 (the same bits as the second
-     * kernel) and applies Out.  No second kernel, at most 16384 tiles a part. */
-    uint32_t kfuse;
 } hb_desc;
 
 /* Gpu::pipeline(&Emitted) (metal/gpu.rs:127-148) for the kernel the

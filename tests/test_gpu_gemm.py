@@ -41,11 +41,6 @@ TILES = {
     "pp_t256x288_b4": dict(bm=256, bn=288, bk=32, wm=4, wn=2, mfma=16, dbuf=3, lds_dma=1, order=1,
                            band=4, sched=1),
     "pp_t128x128": dict(bm=128, bn=128, bk=32, wm=2, wn=4, mfma=16, dbuf=3, lds_dma=1, order=1, sched=1),
-    # split K in one launch (hb_desc.kfuse): the tile's last part adds the parts
-    "pp_t128x160_ksf2": dict(bm=128, bn=160, bk=64, wm=4, wn=2, mfma=16, dbuf=3, lds_dma=1, order=1, sched=1,
-                             ksplit=2, kfuse=1),
-    "pp_t128x160_ksf4": dict(bm=128, bn=160, bk=64, wm=4, wn=2, mfma=16, dbuf=3, lds_dma=1, order=1, sched=1,
-                             ksplit=4, kfuse=1),
     "pp_t128x256_s3": dict(bm=128, bn=256, bk=32, wm=2, wn=4, mfma=16, dbuf=2, lds_dma=1, order=0,
                            sched=1),
     "pp_t256x192_x32_g2": dict(bm=256, bn=192, bk=32, wm=4, wn=2, mfma=32, dbuf=3, lds_dma=1, order=1,
@@ -370,38 +365,3 @@ def test_descriptor_refusals(gpu):
     k = gpu.pipeline(hb.gemm_mma(256, 512, 0, bm=128, bn=128, bk=64, wm=2, wn=2, mfma=16, dbuf=1,
                                  lds_dma=1, w_nt=1))
     assert gpu.kernel_kind(k) == hb.Kind.GEMM and gpu.kernel_name(k).find("_wnt") > 0
-
-
-@pytest.mark.parametrize("ksplit", [2, 4, 8])
-@pytest.mark.parametrize("name,k,n,out", [("qkv", 2560, 4608, 0), ("o", 4096, 2560, 2)])
-def test_split_k_one_launch_equals_two_kernels(gpu, name, k, n, out, ksplit):
-    """kfuse (the tile's last part adds the parts in part order) gives the
-    two-kernel split's bits, launch after launch (its tile counters back at
-    zero), with state rows below the launch's rows, and within the contract."""
-    m, rows = 512, 300
-    x, w = inputs(m, k, n, 0x5EED0500 + k)
-    y0 = hb.normal_bf16(0x5EED0501, 1.0, (m, n))
-    tile = dict(bm=128, bn=160, bk=64, wm=4, wn=2, mfma=16, dbuf=3, lds_dma=1, order=1, sched=1, ksplit=ksplit)
-    two = gpu.pipeline(hb.gemm_mma(k, n, out, **tile))
-    one = gpu.pipeline(hb.gemm_mma(k, n, out, kfuse=1, **tile))
-    assert gpu.kernel_name(one).endswith("_ksf%d_pp" % ksplit), gpu.kernel_name(one)
-    st = gpu.alloc_with(np.array([0, 0, 0, rows], np.uint32))
-    W, X, Y = gpu.alloc_with(w), gpu.alloc_with(x), gpu.alloc(m * n * 2)
-    try:
-        outs = []
-        for kern in (two, one, one, one):
-            gpu.upload(Y, y0)
-            gpu.launch(kern, [hb.r(st), hb.r(W), hb.r(X), hb.r(Y), hb.r(st), hb.r(st)], m)
-            gpu.sync()
-            outs.append(gpu.download(Y, np.uint16, m * n).reshape(m, n))
-        for i, o in enumerate(outs[1:]):
-            assert np.array_equal(o, outs[0]), "launch %d of the one-launch split differs from two kernels" % i
-        assert np.array_equal(outs[1][rows:], y0[rows:])  # rows past state[3] untouched
-        sel = np.array([0, 1, 77, 150, 298, 299])
-        want = orc.gemm(x[sel], w, out, y0[sel] if out == 2 else None)
-        acc = orc.gemm(x[sel], w, orc.OUT_F32) if out == 2 else None
-        check_close(outs[1][sel], want, k, abs_products(x, w, sel), "%s ksf%d" % (name, ksplit), acc=acc,
-                    min_exact=0.98)
-    finally:
-        for b in (st, W, X, Y):
-            gpu.free(b)
