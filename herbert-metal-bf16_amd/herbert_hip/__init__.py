@@ -1035,6 +1035,30 @@ class PrefillAttnProj:
             self.gpu.free(buf)
 
 
+def probe_ids(n):
+    """probe_ids (qwen.rs:2952-2955): the pseudo-random token ids the load's
+    timings run on."""
+    return [1000 + (i * 7919) % 50000 for i in range(n)]
+
+
+def route_probe_rows(ckpt, block, hidden):
+    """route_probe (qwen.rs:2928-2946) as far as the matmul path reaches: the
+    reference prefills `prefill.block` probe ids through the first period of
+    layers, so that the experts are timed on the route its router gives
+    them; here the residual stream those rows start from -- the checkpoint's
+    embedding rows of the probe ids (ids past the vocabulary wrap around) --
+    for MoeBlock, which routes them with the layer's own norm and router
+    before the experts are timed.  The mixer layers before the MoE (attention,
+    DeltaNet) are not part of this library, so their contribution to the
+    rows is missing."""
+    n = ckpt.elements("embed_tokens")
+    if not n or n % hidden:
+        raise HerbertError(HB_ERR_INVALID, "route_probe: no embed_tokens of width %d" % hidden)
+    vocab = n // hidden
+    emb = ckpt.read([("embed_tokens", n)]).reshape(vocab, hidden)
+    return emb[np.array(probe_ids(block), dtype=np.int64) % vocab]
+
+
 def moe_weights_from_checkpoint(gpu, ckpt, layer, experts, hidden, inter, shared_inter):
     """The device weights of a qwen3_5_moe layer's sparse MLP as
     QwenEngine::load uploads them (qwen.rs:788-801): the post norm, the

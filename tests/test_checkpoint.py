@@ -101,3 +101,23 @@ def test_blocks_of(chunk):
         assert got == blocks_of_restated(n, chunk), (n, chunk)
         assert sum(r for _, r in got) == n and all(r <= chunk for _, r in got)
         assert len(got) == math.ceil(n / chunk)
+
+
+def test_probe_ids_are_the_reference_formula():
+    """probe_ids (qwen.rs:2952-2955): 1000 + (i * 7919) % 50000."""
+    ids = hb.probe_ids(10)
+    assert ids == [1000, 8919, 16838, 24757, 32676, 40595, 48514, 6433, 14352, 22271]
+    assert all(1000 <= v < 51000 for v in hb.probe_ids(4096))
+
+
+def test_route_probe_rows_are_the_probe_ids_embeddings(tmp_path):
+    """route_probe's rows: the embedding rows of the probe ids, wrapped
+    around the vocabulary; refused without an embedding of that width."""
+    vocab, h = 97, 16
+    emb = (np.arange(vocab * h, dtype=np.uint32) % 60000).astype(np.uint16).reshape(vocab, h)
+    write_model(str(tmp_path / "m"), [{"model.embed_tokens.weight": ("BF16", emb)}])
+    with hb.Checkpoint(str(tmp_path / "m")) as ck:
+        rows = hb.route_probe_rows(ck, 40, h)
+        assert np.array_equal(rows, emb[np.array(hb.probe_ids(40)) % vocab])
+        with pytest.raises(hb.HerbertError, match="embed_tokens"):
+            hb.route_probe_rows(ck, 4, 24)

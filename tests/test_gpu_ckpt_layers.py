@@ -66,8 +66,11 @@ def test_moe_block_from_checkpoint(gpu, tmp_path):
             "s_gate": hb.normal_bf16(95, 0.02, (SI, H)), "s_up": hb.normal_bf16(96, 0.02, (SI, H)),
             "s_down": hb.normal_bf16(97, 0.02, (H, SI)), "shared_gate": hb.normal_bf16(98, 0.05, (H,))}
     p = PFX % L
+    vocab = 3001  # the probe ids (1000 + 7919 i mod 50000) wrap around it
+    emb = hb.normal_bf16(90, 1.0, (vocab, H))
     write_model(str(tmp_path / "m"), [
-        {p + "post_attention_layernorm.weight": ("BF16", host["post_norm"]),
+        {"model.language_model.embed_tokens.weight": ("BF16", emb),
+         p + "post_attention_layernorm.weight": ("BF16", host["post_norm"]),
          p + "mlp.gate.weight": ("BF16", host["router"]),
          p + "mlp.experts.gate_up_proj": ("BF16", host["w_gate_up"].reshape(E, 2 * MI, H))},
         {p + "mlp.experts.down_proj": ("BF16", host["w_down"].reshape(E, H, MI)),
@@ -75,9 +78,11 @@ def test_moe_block_from_checkpoint(gpu, tmp_path):
          p + "mlp.shared_expert.up_proj.weight": ("BF16", host["s_up"]),
          p + "mlp.shared_expert.down_proj.weight": ("BF16", host["s_down"]),
          p + "mlp.shared_expert_gate.weight": ("BF16", host["shared_gate"].reshape(1, H))}])
-    x0 = hb.normal_bf16(99, 1.0, (rows, H))
     with hb.Checkpoint(str(tmp_path / "m")) as ck:
         w = hb.moe_weights_from_checkpoint(gpu, ck, L, E, H, MI, SI)
+        # route_probe: the experts timed on the route of the probe ids' rows
+        x0 = hb.route_probe_rows(ck, rows, H)
+    assert np.array_equal(x0, emb[(1000 + 7919 * np.arange(rows)) % 50000 % vocab])
     with hb.Engine(gpu, "") as e:
         blk = hb.MoeBlock(gpu, e, E, K_, H, MI, SI, rows, w, x0)
     try:
