@@ -72,6 +72,7 @@ MARK_BYTES = 7 * 4096  # the trace marker fill: 7 workgroups of 256 threads
 # heat, K=20 steps (8 ms) are timed mostly before the ramp.
 HEAT_S = 1.0
 COUNTER_RUN = False
+GRAPH = False  # --graph: the decode steps also timed as recorded graphs
 
 
 # Named regions of the run: each timed region is bracketed by two marker
@@ -237,7 +238,7 @@ def yardstick(steps):
 
 
 def main():
-    global HEAT_S, COUNTER_RUN
+    global HEAT_S, COUNTER_RUN, GRAPH
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
@@ -250,6 +251,8 @@ def main():
     ap.add_argument("--no-matvec", action="store_true")
     ap.add_argument("--no-moe", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--graph", action="store_true",
+                    help="also time each decode step recorded as one HIP graph (not under a profiler)")
     ap.add_argument("--traffic-run", action="store_true")
     ap.add_argument("--traffic-summary", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     ap.add_argument("--counter-run", action="store_true",
@@ -282,6 +285,7 @@ def main():
 
     HEAT_S = 0.0 if args.counter_run else max(0.0, args.heat)
     COUNTER_RUN = args.counter_run
+    GRAPH = args.graph
     import herbert_hip as hb
     g = hb.Gpu(0)
     log("[gpu]", g.summary())
@@ -910,26 +914,30 @@ def bench_matvec(g, e, hb):
         reps = 20
         with region(g, "decode_m%d" % mv_m):
             t = g.time_ops(ops, reps) / reps
-        # The same step recorded as one HIP graph (the reference encodes a
-        # step's ops in one command buffer, qwen.rs:3177), timed the same way.
-        gr = g.graph(ops)
-        try:
-            gr.time(3)
-            heat(g, ops)
-            gr.time(50)
-            tg = gr.time(reps) / reps
-        finally:
-            gr.free()
-        forms = {"stream": t, "graph": tg}
+        forms = {"stream": t}
+        if GRAPH:
+            # The same step recorded as one HIP graph (the reference encodes a
+            # step's ops in one command buffer, qwen.rs:3177), timed the same
+            # way (--graph; measured no faster than the stream, and the
+            # profiler's kernel trace does not survive a graph launch).
+            gr = g.graph(ops)
+            try:
+                gr.time(3)
+                heat(g, ops)
+                gr.time(50)
+                forms["graph"] = gr.time(reps) / reps
+            finally:
+                gr.free()
         best = min(forms, key=forms.get)
         best_gbs = nbytes / forms[best] / 1e9
         r = {"value": round(best_gbs, 1), "unit": "GB/s", "frac": round(best_gbs / HBM_PEAK, 4), "peak": HBM_PEAK,
              "form": best,
              "ms_per_step": round(forms[best] * 1e3, 4), "m": mv_m, "layers": DECODE_LAYERS,
              "bytes_per_step": nbytes, "kernels": {nm: g.kernel_name(kern[nm]) for nm in kern}}
-        for nm, tt in forms.items():
-            r[nm] = {"ms_per_step": round(tt * 1e3, 4), "gbs": round(nbytes / tt / 1e9, 1),
-                     "frac": round(nbytes / tt / 1e9 / HBM_PEAK, 4)}
+        if len(forms) > 1:
+            for nm, tt in forms.items():
+                r[nm] = {"ms_per_step": round(tt * 1e3, 4), "gbs": round(nbytes / tt / 1e9, 1),
+                         "frac": round(nbytes / tt / 1e9 / HBM_PEAK, 4)}
         if mv_m == 1:
             # the lm_head alone, two copies in turn (2 x 778 MB: no copy is
             # still in the 256 MB last-level cache when it is read again)
