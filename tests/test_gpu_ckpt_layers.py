@@ -82,7 +82,7 @@ def test_moe_block_from_checkpoint(gpu, tmp_path):
         w = hb.moe_weights_from_checkpoint(gpu, ck, L, E, H, MI, SI)
         # route_probe: the experts timed on the route of the probe ids' rows
         x0 = hb.route_probe_rows(ck, rows, H)
-    assert np.array_equal(x0, emb[(1000 + 7919 * np.arange(rows)) % 50000 % vocab])
+    assert np.array_equal(x0, emb[(1000 + (7919 * np.arange(rows)) % 50000) % vocab])
     with hb.Engine(gpu, "") as e:
         blk = hb.MoeBlock(gpu, e, E, K_, H, MI, SI, rows, w, x0)
     try:
