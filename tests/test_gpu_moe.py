@@ -225,3 +225,62 @@ def test_grouped_gate_up_swiglu_fused(gpu, bm, bn, wm, wn):
         wr = w[ex[i] * 2 * inter:(ex[i] + 1) * 2 * inter]
         check_close(egu[p:p + 1], orc.gemm(xr[i:i + 1], wr), hidden, abs_products(xr[i:i + 1], wr),
                     "pair %d" % p)
+
+
+@pytest.mark.parametrize("tname,bm", [("m128_w2x2", 128), ("m16_dma", 16),
+                                      ("m128_n256_w8_s3_nf_wnt", 128)])
+def test_skewed_route(gpu, tname, bm):
+    """A route a trained router could give: three experts chosen by every
+    token (512 rows each: several tiles of one expert), one by half the
+    tokens, most experts by none.  The sort (both forms) against the oracle,
+    the grouped gate|up / down within the contract on every output, and the
+    combine of the GPU's slot rows bit for bit."""
+    rows = 512
+    scores = hb.normal_bf16(0x5EED0600, 1.0, (rows, E)).astype(np.uint32)
+    f = (scores << 16).view(np.float32)
+    f[:, [3, 7, 200]] += 8.0
+    f[: rows // 2, 11] += 8.0
+    cold = np.setdiff1d(np.arange(128, E), [200])
+    f[:, cold] -= 8.0  # never chosen
+    scores = orc_round(f)
+    route = orc.route(scores, TOPK)
+    counts = np.bincount(route[:, :TOPK].ravel(), minlength=E)
+    assert counts[3] == counts[7] == counts[200] == rows and counts[11] >= rows // 2
+    assert (counts == 0).sum() > E // 4
+    lst, tiles = sort_gpu(gpu, route, TOPK, E, bm, rows)
+    wl, wt = orc.moe_sort(route, TOPK, E, bm)
+    used = 1 + 3 * int(wt[0])
+    assert np.array_equal(lst, wl) and np.array_equal(tiles[:used], wt[:used])
+    al, at = sort_gpu(gpu, route, TOPK, E, bm, rows, atomic=True)
+    assert np.array_equal(at[:used], wt[:used])
+    assert np.array_equal(route[al // TOPK, al % TOPK], route[wl // TOPK, wl % TOPK])
+
+    x = hb.normal_bf16(0x5EED0601, 1.0, (rows, H))
+    wgu = hb.normal_bf16(0x5EED0602, 0.02, (E * 2 * MI, H))
+    got = experts_run(gpu, x, wgu, wl, wt, H, 2 * MI, hb.Rows.Gather, rows, bm, **EXPERT_TILES[tname])
+    want = orc.experts_gemm(x, wgu, wl, wt, H, 2 * MI, 1, TOPK, rows * TOPK)
+    ex = route[wl // TOPK, wl % TOPK]
+    ap = np.empty(want.shape)
+    for e in np.unique(ex):
+        sel = np.nonzero(ex == e)[0]
+        ap[sel] = abs_products(x[wl[sel] // TOPK], wgu[e * 2 * MI:(e + 1) * 2 * MI])
+    check_close(got, want, H, ap, "skewed gate_up " + tname, min_exact=0.98)
+
+    h = orc.swiglu(want, MI)
+    wd = hb.normal_bf16(0x5EED0603, 0.02, (E * H, MI))
+    ey = experts_run(gpu, h, wd, wl, wt, MI, H, hb.Rows.Scatter, rows, bm, **EXPERT_TILES[tname])
+    want_ey = orc.experts_gemm(h, wd, wl, wt, MI, H, 2, TOPK, rows * TOPK)
+    apd = np.empty(want_ey.shape)
+    for e in np.unique(ex):
+        sel = np.nonzero(ex == e)[0]
+        apd[wl[sel]] = abs_products(h[sel], wd[e * H:(e + 1) * H])
+    check_close(ey, want_ey, MI, apd, "skewed down " + tname, min_exact=0.98)
+    d = hb.Desc(kind=hb.Kind.COMBINE, n=H, top_k=TOPK)
+    out = launch(gpu, d, [ey, route, rows * H * 2], rows, {2: (np.uint16, rows * H)})[2]
+    assert np.array_equal(out.reshape(rows, H), orc.combine(ey, route, TOPK, H))
+
+
+def orc_round(f):
+    """bf16 bits of float32 values, round to nearest even (core/bf16.rs:13-23)."""
+    b = np.ascontiguousarray(f, np.float32).view(np.uint32)
+    return ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
